@@ -1,0 +1,211 @@
+// Device-side numerics shared by every gfx950 kernel in libkudacuda.
+//
+// Every reduction below has ONE fixed order (lane -> chunk mapping, per-lane
+// accumulator split, butterfly stages).  The decode path's results are a pure
+// function of its inputs, so greedy tokens are reproducible run to run and can
+// be matched bit for bit by a host restatement that follows the same order.
+//
+// Conventions (wave64):
+//  * NF4 "chunk": 16 packed bytes = 32 consecutive logical elements; chunk c of
+//    a row holds elements [32c, 32c+32) and uses absmax block c/2 (blocksize
+//    64).  Byte i of a chunk carries element 2i in its high nibble and 2i+1 in
+//    its low nibble (bitsandbytes packing, reference
+//    kernels/common/nf4_device.cuh:36-39).
+//  * chunk dot: four accumulators, one per 32-bit word (8 elements each),
+//    sequential fmaf inside a word, combined as (a0+a1)+(a2+a3), then multiplied
+//    by the block's absmax.
+//  * wave_sum: butterfly v += shfl_xor(v, o) for o = 32,16,8,4,2,1; the result
+//    is identical in every lane because IEEE addition is commutative.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kc {
+
+// bitsandbytes NF4 codebook (the 16 fp32 values of the format; reference
+// kernels/common/nf4_device.cuh:10-27).  Kept as exact hex literals.
+__device__ constexpr float kNf4Codebook[16] = {
+    -0x1.000000p+0f, -0x1.647362p-1f, -0x1.0cd660p-1f, -0x1.946540p-2f,
+    -0x1.23449ap-2f, -0x1.7a6a7ep-3f, -0x1.74f0e2p-4f, 0x0.0p+0f,
+    0x1.45f5fep-4f,  0x1.4995c6p-3f,  0x1.f809bap-3f,  0x1.5a0674p-2f,
+    0x1.c34970p-2f,  0x1.200f56p-1f,  0x1.722766p-1f,  0x1.000000p+0f,
+};
+
+constexpr float kLog2e = 0x1.715476p+0f;  // fp32(log2(e))
+
+// ---------------------------------------------------------------- conversions
+__device__ __forceinline__ float bf16_to_f32(uint16_t v) {
+    return __uint_as_float(static_cast<uint32_t>(v) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16; NaN becomes a quiet NaN with its sign.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) {
+        return static_cast<uint16_t>((u >> 16) | 0x0040u);
+    }
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t v) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, v));
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+// Activation element types travel as 16-bit storage; the tag picks the
+// conversion.  Bf16 is the decode path's type, F16 serves the reference's
+// fp16 entry points.
+struct Bf16 {
+    static __device__ __forceinline__ float load(uint16_t v) { return bf16_to_f32(v); }
+    static __device__ __forceinline__ uint16_t store(float f) { return f32_to_bf16(f); }
+};
+struct F16 {
+    static __device__ __forceinline__ float load(uint16_t v) { return f16_to_f32(v); }
+    static __device__ __forceinline__ uint16_t store(float f) { return f32_to_f16(f); }
+};
+
+// Unpack 8 consecutive 16-bit elements held in a uint4.
+template <typename T>
+__device__ __forceinline__ void unpack8(const uint4 v, float* out) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        out[2 * i] = T::load(static_cast<uint16_t>(w[i] & 0xffffu));
+        out[2 * i + 1] = T::load(static_cast<uint16_t>(w[i] >> 16));
+    }
+}
+
+// ---------------------------------------------------------------------- exp2
+// 2^y by exact reduction y = n + f (n = rint(y), |f| <= 1/2, f exact) and the
+// degree-7 Taylor polynomial of e^(f ln 2) in Horner form, scaled by ldexp.
+// Results below 2^-125 flush to +0 (so no subnormal is ever produced) and
+// y >= 128 gives +inf.  Max error about 2 ulp over the whole range.
+__device__ __forceinline__ float exp2_fixed(float y) {
+    if (!(y >= -125.0f)) {
+        return (y != y) ? y : 0.0f;
+    }
+    if (y >= 128.0f) {
+        return __builtin_huge_valf();
+    }
+    const float n = rintf(y);
+    const float f = y - n;
+    float p = 0x1.ffcbfcp-17f;
+    p = fmaf(p, f, 0x1.430912p-13f);
+    p = fmaf(p, f, 0x1.5d87fep-10f);
+    p = fmaf(p, f, 0x1.3b2ab6p-7f);
+    p = fmaf(p, f, 0x1.c6b08ep-5f);
+    p = fmaf(p, f, 0x1.ebfbe0p-3f);
+    p = fmaf(p, f, 0x1.62e430p-1f);
+    p = fmaf(p, f, 1.0f);
+    return ldexpf(p, static_cast<int>(n));
+}
+
+// silu(g) = g / (1 + e^-g), with e^-g = exp2_fixed(g * -log2e).
+__device__ __forceinline__ float silu_fixed(float g) {
+    const float e = exp2_fixed(g * -kLog2e);
+    return g / (1.0f + e);
+}
+
+// ---------------------------------------------------------------- reductions
+__device__ __forceinline__ float wave_sum(float v) {
+    v += __shfl_xor(v, 32, 64);
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 8, 64);
+    v += __shfl_xor(v, 4, 64);
+    v += __shfl_xor(v, 2, 64);
+    v += __shfl_xor(v, 1, 64);
+    return v;
+}
+
+// Butterfly over the 16 lanes of a row (o = 8,4,2,1).
+__device__ __forceinline__ float group16_sum(float v) {
+    v += __shfl_xor(v, 8, 64);
+    v += __shfl_xor(v, 4, 64);
+    v += __shfl_xor(v, 2, 64);
+    v += __shfl_xor(v, 1, 64);
+    return v;
+}
+
+// ------------------------------------------------------------------ NF4 dots
+// Dot of one 32-element chunk with x[0..31] (already in fp32), before the
+// absmax multiply.  cb points at the codebook (LDS copy).
+__device__ __forceinline__ float nf4_chunk_dot_raw(const uint4 pk, const float* x, const float* cb) {
+    const uint32_t w[4] = {pk.x, pk.y, pk.z, pk.w};
+    float a[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const uint32_t byte = (w[i] >> (8 * b)) & 0xffu;
+            acc = fmaf(x[8 * i + 2 * b], cb[byte >> 4], acc);
+            acc = fmaf(x[8 * i + 2 * b + 1], cb[byte & 0xfu], acc);
+        }
+        a[i] = acc;
+    }
+    return (a[0] + a[1]) + (a[2] + a[3]);
+}
+
+// Sum of squares of 32 consecutive elements, same accumulator split as a
+// chunk dot.
+__device__ __forceinline__ float sumsq32(const float* x) {
+    float a[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            acc = fmaf(x[8 * i + j], x[8 * i + j], acc);
+        }
+        a[i] = acc;
+    }
+    return (a[0] + a[1]) + (a[2] + a[3]);
+}
+
+// 1 / sqrt(sumsq / n + eps), every step correctly rounded.
+__device__ __forceinline__ float inv_rms(float sumsq, float n, float eps) {
+    return 1.0f / sqrtf(sumsq / n + eps);
+}
+
+// Load the 32 activation elements of chunk `lane` (elements [32*lane, +32))
+// from a 16-bit vector, RMS-normalise them against the whole 2048-element
+// vector and return them in fp32: x_n = (x * inv_rms) * gamma.  When gamma is
+// null the raw values are returned.
+template <typename T>
+__device__ __forceinline__ void load_norm_x2048(const uint16_t* __restrict__ x,
+                                                const uint16_t* __restrict__ gamma,
+                                                float eps, int lane, float* xn) {
+    const uint4* xv = reinterpret_cast<const uint4*>(x) + lane * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        unpack8<T>(xv[i], xn + 8 * i);
+    }
+    if (gamma == nullptr) {
+        return;
+    }
+    const float ss = wave_sum(sumsq32(xn));
+    const float r = inv_rms(ss, 2048.0f, eps);
+    float g[32];
+    const uint4* gv = reinterpret_cast<const uint4*>(gamma) + lane * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        unpack8<T>(gv[i], g + 8 * i);
+    }
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        xn[j] = (xn[j] * r) * g[j];
+    }
+}
+
+__device__ __forceinline__ void load_codebook_lds(float* cb) {
+    if (threadIdx.x < 16) {
+        cb[threadIdx.x] = kNf4Codebook[threadIdx.x];
+    }
+}
+
+}  // namespace kc

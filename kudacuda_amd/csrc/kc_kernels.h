@@ -1,0 +1,117 @@
+// Internal launch interface between the C-ABI runtime (kc_runtime.hip) and
+// the gfx950 kernels.  Nothing here is exported from libkudacuda.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kc {
+
+enum class Act { kBf16 = 0, kF16 = 1 };
+
+// ------------------------------------------------------------------- NF4 rows
+// One launch of the K = 2048 NF4 row kernel.  `mode` selects the row set and
+// the epilogue:
+//   kGemv      : y[r]   = T(dot_r + bias[r])            (rows 0..n0)
+//                with residual: y[r] = T(res[r] + T(dot_r))
+//   kQkv       : q/k/v  = T(dot + bias) for Wq, Wk, Wv  (no rotary)
+//   kQkvRope   : q = T(rope(dot + bias)); k, v written into the KV cache at
+//                the device-resident position control[0]
+//   kSwiGlu    : h[r]   = T(silu(gate_r) * up_r)
+enum class RowMode { kGemv = 0, kQkv = 1, kQkvRope = 2, kSwiGlu = 3 };
+
+struct Nf4RowsArgs {
+    const uint16_t* x = nullptr;      // activation [2048], 16-bit
+    const uint16_t* gamma = nullptr;  // RMSNorm weight [2048] or null (no norm)
+    float eps = 1e-6f;
+    const uint8_t* w[3] = {nullptr, nullptr, nullptr};
+    const float* absmax[3] = {nullptr, nullptr, nullptr};
+    const uint16_t* bias[3] = {nullptr, nullptr, nullptr};
+    uint16_t* out[3] = {nullptr, nullptr, nullptr};
+    int64_t rows[3] = {0, 0, 0};
+    const uint16_t* residual = nullptr;  // kGemv only; may alias out[0]
+    float* norm_out = nullptr;           // optional fp32 copy of the normalised x
+    // kQkvRope state
+    const float* rope_cos = nullptr;  // [capacity, 64]
+    const float* rope_sin = nullptr;
+    const int32_t* control = nullptr;  // control[0] = position of this token
+    int64_t capacity = 0;
+    uint16_t* kcache = nullptr;  // [2, capacity, 128]
+    uint16_t* vcache = nullptr;
+    // optional embedding gather for the first layer: x := embed[tokens[pos]]
+    const uint16_t* embed = nullptr;
+    const int32_t* tokens = nullptr;
+    int64_t vocab = 0;
+    uint16_t* hidden_out = nullptr;  // receives the gathered row
+};
+
+hipError_t launch_nf4_rows2048(RowMode mode, Act act, const Nf4RowsArgs& args, hipStream_t stream);
+
+// K = 11008 NF4 GEMV (Qwen2.5-3B down projection).  y[r] = T(dot_r) or, with
+// a residual, y[r] = T(res[r] + T(dot_r)).
+struct Nf4DownArgs {
+    const uint16_t* x = nullptr;  // [11008]
+    const uint8_t* w = nullptr;
+    const float* absmax = nullptr;
+    const uint16_t* residual = nullptr;
+    uint16_t* out = nullptr;
+    int64_t rows = 0;
+};
+hipError_t launch_nf4_down11008(Act act, const Nf4DownArgs& args, hipStream_t stream);
+
+// Blockwise NF4 quantisation (blocksize 64) of n elements (n % 64 == 0).
+hipError_t launch_nf4_quantize_f32(const float* src, int64_t n, uint8_t* packed, float* absmax, hipStream_t stream);
+hipError_t launch_nf4_quantize_bf16(const uint16_t* src, int64_t n, uint8_t* packed, float* absmax, hipStream_t stream);
+// out_kind: 0 = fp32, 1 = bf16, 2 = fp16
+hipError_t launch_nf4_dequantize(const uint8_t* packed, const float* absmax, int64_t n, int64_t blocksize,
+                                 int out_kind, void* out, hipStream_t stream);
+
+// ------------------------------------------------------------------------ GQA
+// Split-KV grouped-query decode attention, 16 query heads / 2 KV heads /
+// head_dim 128.  `chunk` tokens per split (multiple of 64).  kv_len is read
+// from kv_len_device when non-null, else kv_len_host is used.
+struct GqaArgs {
+    const uint16_t* q = nullptr;   // [16,128]
+    const uint16_t* k = nullptr;   // [2, capacity, 128]
+    const uint16_t* v = nullptr;
+    uint16_t* out = nullptr;       // [16,128]
+    float* partials = nullptr;     // [16, max_splits, 130]
+    uint32_t* counters = nullptr;  // [2], zero between calls
+    const int32_t* kv_len_device = nullptr;
+    int32_t kv_len_offset = 0;     // added to *kv_len_device (decoder: pos + 1)
+    int64_t kv_len_host = 0;
+    int64_t capacity = 0;          // row stride of the cache
+    int64_t max_splits = 0;        // grid size per KV head
+    int64_t chunk = 64;
+    float qk_scale_log2 = 0.0f;    // scale * log2(e)
+};
+hipError_t launch_gqa_decode(Act act, const GqaArgs& args, hipStream_t stream);
+int64_t gqa_chunk_for(int64_t tokens);  // chunk rule shared with the host oracle
+
+// ------------------------------------------------------------- lm_head/argmax
+struct LmHeadArgs {
+    const uint16_t* x = nullptr;      // hidden [2048] bf16
+    const uint16_t* gamma = nullptr;  // final norm weight or null
+    float eps = 1e-6f;
+    const uint16_t* weight = nullptr; // [vocab, 2048] bf16
+    int64_t vocab = 0;
+    uint16_t* logits = nullptr;       // [vocab] bf16 (may be null)
+    float* block_best = nullptr;      // [2 * grid] (value, index-as-bits)
+    uint32_t* counter = nullptr;      // zero between calls
+    int32_t* argmax_out = nullptr;    // receives the token id (may be null)
+    // decode bookkeeping (null for a plain lm_head call)
+    int32_t* control = nullptr;       // [0]=step [1]=prompt_len [2]=token capacity
+    int32_t* tokens = nullptr;
+};
+hipError_t launch_lm_head_argmax(const LmHeadArgs& args, hipStream_t stream);
+int64_t lm_head_workspace_floats();  // size of block_best
+
+// ------------------------------------------------------------------ misc ops
+hipError_t launch_vector_add(const float* a, const float* b, float* out, int64_t n, hipStream_t stream);
+hipError_t launch_rmsnorm_f32(const float* x, const float* w, float* y, int64_t rows, int64_t hidden, float eps,
+                              hipStream_t stream);
+hipError_t launch_dense_rmsnorm_qkv_f16(const uint16_t* x, const uint16_t* gamma, const uint16_t* w,
+                                        const uint16_t* bias, uint16_t* out, int64_t rows, int64_t hidden,
+                                        float eps, hipStream_t stream);
+
+}  // namespace kc

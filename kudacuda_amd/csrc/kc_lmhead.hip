@@ -1,0 +1,224 @@
+// Dense bf16 lm_head GEMV (tied embedding, vocab x 2048) fused with the final
+// RMSNorm, bf16 logit rounding and a device-side greedy argmax.
+//
+// One wave per vocabulary row: lane l reads 16-byte chunks l, l+64, l+128,
+// l+192 of the 4 KiB row (every wave load is a contiguous 1 KiB), keeps one
+// accumulator per chunk and combines them as (a0+a1)+(a2+a3) before the wave
+// butterfly.  The logit is rounded to bf16 (the model's logits dtype) and the
+// argmax runs on the rounded values with the lowest index winning ties, as
+// torch.argmax does on the reference's logits
+// (tools/benchmark/benchmark_gemma.py:350).  Block winners go to a small
+// workspace and the last block (device-scope ticket) picks the token.
+//
+// When `control` is given the launch also does the per-token decode
+// bookkeeping on device: during the prompt (step + 1 < prompt_len) the GEMV is
+// skipped and the next prompt token stays in place; otherwise the winner is
+// written to tokens[step + 1]; step then advances.  This removes the host
+// argmax/.item() round trip the reference pays per token
+// (tools/benchmark/benchmark_gemma.py:328-352).
+#include "kc_device.h"
+#include "kc_kernels.h"
+
+namespace kc {
+namespace {
+
+constexpr int kLmThreads = 256;
+constexpr int kLmMaxBlocks = 1024;
+
+__device__ __forceinline__ bool better(float v, int32_t i, float bv, int32_t bi) {
+    return v > bv || (v == bv && i < bi);
+}
+
+__device__ __forceinline__ float row_dot(const uint4* w, const float* xn) {
+    float a[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        float wf[8];
+        unpack8<Bf16>(w[c], wf);
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            acc = fmaf(xn[8 * c + j], wf[j], acc);
+        }
+        a[c] = acc;
+    }
+    return (a[0] + a[1]) + (a[2] + a[3]);
+}
+
+__global__ __launch_bounds__(kLmThreads) void lm_head_kernel(LmHeadArgs a) {
+    __shared__ float s_val[kLmThreads / 64];
+    __shared__ int32_t s_idx[kLmThreads / 64];
+    __shared__ int s_last;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+
+    int32_t step = 0;
+    bool active = true;
+    if (a.control != nullptr) {
+        step = a.control[0];
+        active = step + 1 >= a.control[1];
+    }
+
+    float best = -__builtin_huge_valf();
+    int32_t best_idx = 0x7fffffff;
+    if (active) {
+        // Final RMSNorm: inverse RMS over elements [32l, 32l+32) per lane,
+        // then the lane's dot elements 8(l + 64c) + j, normalised the same way.
+        float xs[32];
+        const uint4* xv = reinterpret_cast<const uint4*>(a.x);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            unpack8<Bf16>(xv[lane * 4 + i], xs + 8 * i);
+        }
+        float r = 1.0f;
+        if (a.gamma != nullptr) {
+            r = inv_rms(wave_sum(sumsq32(xs)), 2048.0f, a.eps);
+        }
+        float xn[32];
+        const uint4* gv = reinterpret_cast<const uint4*>(a.gamma);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            unpack8<Bf16>(xv[lane + 64 * c], xn + 8 * c);
+            if (a.gamma != nullptr) {
+                float gf[8];
+                unpack8<Bf16>(gv[lane + 64 * c], gf);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    xn[8 * c + j] = (xn[8 * c + j] * r) * gf[j];
+                }
+            }
+        }
+
+        const int64_t nwaves = static_cast<int64_t>(gridDim.x) * (kLmThreads / 64);
+        int64_t row = static_cast<int64_t>(blockIdx.x) * (kLmThreads / 64) + wave;
+        uint4 w[4];
+        if (row < a.vocab) {
+            const uint4* src = reinterpret_cast<const uint4*>(a.weight + row * 2048);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                w[c] = src[lane + 64 * c];
+            }
+        }
+        while (row < a.vocab) {
+            const int64_t next = row + nwaves;
+            uint4 nw[4];
+            if (next < a.vocab) {
+                const uint4* src = reinterpret_cast<const uint4*>(a.weight + next * 2048);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    nw[c] = src[lane + 64 * c];
+                }
+            }
+            const float sum = wave_sum(row_dot(w, xn));
+            const uint16_t lb = f32_to_bf16(sum);
+            const float v = bf16_to_f32(lb);
+            if (lane == 0 && a.logits != nullptr) {
+                a.logits[row] = lb;
+            }
+            if (better(v, static_cast<int32_t>(row), best, best_idx)) {
+                best = v;
+                best_idx = static_cast<int32_t>(row);
+            }
+            row = next;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                w[c] = nw[c];
+            }
+        }
+        if (lane == 0) {
+            s_val[wave] = best;
+            s_idx[wave] = best_idx;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            for (int i = 1; i < kLmThreads / 64; ++i) {
+                if (better(s_val[i], s_idx[i], best, best_idx)) {
+                    best = s_val[i];
+                    best_idx = s_idx[i];
+                }
+            }
+            a.block_best[2 * blockIdx.x] = best;
+            a.block_best[2 * blockIdx.x + 1] = __int_as_float(best_idx);
+        }
+    }
+
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t prev = atomicAdd(a.counter, 1u);
+        s_last = prev == gridDim.x - 1 ? 1 : 0;
+    }
+    __syncthreads();
+    if (s_last == 0) {
+        return;
+    }
+    __threadfence();
+    if (active) {
+        best = -__builtin_huge_valf();
+        best_idx = 0x7fffffff;
+        for (int b = threadIdx.x; b < static_cast<int>(gridDim.x); b += kLmThreads) {
+            const float v = a.block_best[2 * b];
+            const int32_t i = __float_as_int(a.block_best[2 * b + 1]);
+            if (better(v, i, best, best_idx)) {
+                best = v;
+                best_idx = i;
+            }
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            const float ov = __shfl_xor(best, o, 64);
+            const int32_t oi = __shfl_xor(best_idx, o, 64);
+            if (better(ov, oi, best, best_idx)) {
+                best = ov;
+                best_idx = oi;
+            }
+        }
+        if (lane == 0) {
+            s_val[wave] = best;
+            s_idx[wave] = best_idx;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            for (int i = 1; i < kLmThreads / 64; ++i) {
+                if (better(s_val[i], s_idx[i], best, best_idx)) {
+                    best = s_val[i];
+                    best_idx = s_idx[i];
+                }
+            }
+            if (best_idx < 0 || best_idx >= a.vocab) {
+                best_idx = 0;  // every logit was NaN
+            }
+        }
+    }
+    if (threadIdx.x == 0) {
+        if (active && a.argmax_out != nullptr) {
+            a.argmax_out[0] = best_idx;
+        }
+        if (a.control != nullptr) {
+            const int32_t next = step + 1;
+            if (active && next < a.control[2]) {
+                a.tokens[next] = best_idx;
+            }
+            a.control[0] = next;
+        }
+        a.counter[0] = 0u;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_lm_head_argmax(const LmHeadArgs& a, hipStream_t stream) {
+    int64_t blocks = (a.vocab + (kLmThreads / 64) - 1) / (kLmThreads / 64);
+    if (blocks > kLmMaxBlocks) {
+        blocks = kLmMaxBlocks;
+    }
+    if (blocks < 1) {
+        blocks = 1;
+    }
+    hipLaunchKernelGGL(lm_head_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kLmThreads), 0, stream, a);
+    return hipGetLastError();
+}
+
+int64_t lm_head_workspace_floats() { return 2 * kLmMaxBlocks; }
+
+}  // namespace kc

@@ -1,0 +1,440 @@
+// NF4 kernels for gfx950: blockwise quantise / dequantise, the K = 2048 row
+// family (GEMV, fused RMSNorm+QKV(+bias), fused QKV+RoPE+KV-cache write,
+// fused gate/up SwiGLU) and the K = 11008 down projection.
+//
+// Design (wave64, bandwidth-bound, no MFMA because M = 1):
+//  * one wave owns a whole 2048-wide row: lane l streams the 16 packed bytes
+//    of chunk l with one 128-bit load, so a wave load is one contiguous
+//    1 KiB row (fully coalesced) and the lane's 32 activations stay in
+//    registers for every row the wave visits;
+//  * the 16-entry fp32 codebook lives in LDS (16 distinct banks: a lookup is
+//    never a bank conflict);
+//  * the RMSNorm is recomputed per wave from the 4 KiB input (an L2 hit after
+//    the first wave) so no block barrier or separate norm launch is needed;
+//  * each wave prefetches its next task's rows before reducing the current
+//    one, keeping two rows per lane in flight.
+// Semantics follow the reference's tiled NF4 kernels
+// (kernels/common/nf4_tiled_gemv.cuh:61-168: norm in fp32, dot in fp32,
+// bias added in fp32 before the single output rounding) and its SwiGLU
+// (kernels/common/nf4_swiglu_bf16.cuh:61-164: silu(g) * u in fp32).
+#include "kc_device.h"
+#include "kc_kernels.h"
+
+namespace kc {
+namespace {
+
+constexpr int kRowsThreads = 256;
+
+// Decision points between adjacent codebook values: fp32 of the fp64
+// midpoint.  A scaled value s maps to the number of midpoints it exceeds, so
+// an exact tie goes to the lower code.
+__device__ constexpr float kNf4Mid[15] = {
+    -0x1.b239b0p-1f, -0x1.38a4e0p-1f, -0x1.d70900p-2f, -0x1.5bd4ecp-2f, -0x1.e079d8p-3f,
+    -0x1.1a7178p-3f, -0x1.74f0e2p-5f, 0x1.45f5fep-5f,  0x1.ec90c4p-4f,  0x1.a0cfc0p-3f,
+    0x1.2b05a8p-2f,  0x1.8ea7f2p-2f,  0x1.00da08p-1f,  0x1.491b5ep-1f,  0x1.b913b4p-1f,
+};
+
+struct RowPair {
+    int m0 = 0, m1 = 0;      // matrix index of each row
+    int64_t r0 = 0, r1 = 0;  // row within its matrix
+    bool has1 = false;
+};
+
+template <RowMode MODE>
+__device__ __forceinline__ RowPair map_task(const Nf4RowsArgs& a, int64_t task) {
+    RowPair p;
+    if constexpr (MODE == RowMode::kGemv) {
+        p.r0 = 2 * task;
+        p.r1 = 2 * task + 1;
+        p.has1 = p.r1 < a.rows[0];
+    } else if constexpr (MODE == RowMode::kSwiGlu) {
+        p.m0 = 0;
+        p.m1 = 1;
+        p.r0 = task;
+        p.r1 = task;
+        p.has1 = true;
+    } else {
+        // Q, K, V rows paired as (d, d + 64) inside each 128-row head so the
+        // rotary rotation of a pair happens in registers.
+        int64_t j = task;
+        int m = 0;
+        while (m < 2 && j >= a.rows[m] / 2) {
+            j -= a.rows[m] / 2;
+            ++m;
+        }
+        const int64_t head = j / 64;
+        const int64_t d = j % 64;
+        p.m0 = m;
+        p.m1 = m;
+        p.r0 = head * 128 + d;
+        p.r1 = head * 128 + d + 64;
+        p.has1 = true;
+    }
+    return p;
+}
+
+__device__ __forceinline__ void fetch_row(const Nf4RowsArgs& a, int m, int64_t r, int lane, uint4& pk, float& am) {
+    pk = reinterpret_cast<const uint4*>(a.w[m] + r * 1024)[lane];
+    am = a.absmax[m][r * 32 + (lane >> 1)];
+}
+
+template <typename T, RowMode MODE>
+__global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs a, int64_t ntasks) {
+    __shared__ float cb[16];
+    load_codebook_lds(cb);
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int64_t waves_per_block = kRowsThreads / 64;
+    const int64_t nwaves = static_cast<int64_t>(gridDim.x) * waves_per_block;
+    int64_t task = static_cast<int64_t>(blockIdx.x) * waves_per_block + wave;
+
+    int64_t pos = 0;
+    if constexpr (MODE == RowMode::kQkvRope) {
+        pos = a.control[0];
+        pos = pos < 0 ? 0 : (pos >= a.capacity ? a.capacity - 1 : pos);
+    }
+    const uint16_t* x = a.x;
+    if (a.embed != nullptr) {
+        // tokens[] holds control[2] entries; never read past it
+        const int64_t tok_cap = a.control[2];
+        const int64_t tpos = pos < tok_cap ? pos : (tok_cap > 0 ? tok_cap - 1 : 0);
+        int64_t tok = a.tokens[tpos];
+        tok = tok < 0 ? 0 : (tok >= a.vocab ? a.vocab - 1 : tok);
+        x = a.embed + tok * 2048;
+    }
+
+    // Issue the first task's weight loads before the norm so HBM latency
+    // overlaps the activation work.
+    RowPair cur;
+    uint4 pk0 = make_uint4(0, 0, 0, 0), pk1 = make_uint4(0, 0, 0, 0);
+    float am0 = 0.0f, am1 = 0.0f;
+    if (task < ntasks) {
+        cur = map_task<MODE>(a, task);
+        fetch_row(a, cur.m0, cur.r0, lane, pk0, am0);
+        if (cur.has1) {
+            fetch_row(a, cur.m1, cur.r1, lane, pk1, am1);
+        }
+    }
+
+    float xn[32];
+    load_norm_x2048<T>(x, a.gamma, a.eps, lane, xn);
+    if (blockIdx.x == 0 && wave == 0) {
+        if (a.hidden_out != nullptr) {
+            const uint4* src = reinterpret_cast<const uint4*>(x) + lane * 4;
+            uint4* dst = reinterpret_cast<uint4*>(a.hidden_out) + lane * 4;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                dst[i] = src[i];
+            }
+        }
+        if (a.norm_out != nullptr) {
+            float4* dst = reinterpret_cast<float4*>(a.norm_out) + lane * 8;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                dst[i] = make_float4(xn[4 * i], xn[4 * i + 1], xn[4 * i + 2], xn[4 * i + 3]);
+            }
+        }
+    }
+    __syncthreads();  // codebook visible
+
+    while (task < ntasks) {
+        const int64_t next = task + nwaves;
+        RowPair nxt;
+        uint4 npk0 = make_uint4(0, 0, 0, 0), npk1 = make_uint4(0, 0, 0, 0);
+        float nam0 = 0.0f, nam1 = 0.0f;
+        if (next < ntasks) {
+            nxt = map_task<MODE>(a, next);
+            fetch_row(a, nxt.m0, nxt.r0, lane, npk0, nam0);
+            if (nxt.has1) {
+                fetch_row(a, nxt.m1, nxt.r1, lane, npk1, nam1);
+            }
+        }
+
+        float d0 = wave_sum(nf4_chunk_dot_raw(pk0, xn, cb) * am0);
+        float d1 = 0.0f;
+        if (cur.has1) {
+            d1 = wave_sum(nf4_chunk_dot_raw(pk1, xn, cb) * am1);
+        }
+
+        if constexpr (MODE == RowMode::kGemv) {
+            if (lane < 2 && (lane == 0 || cur.has1)) {
+                const int64_t r = lane == 0 ? cur.r0 : cur.r1;
+                float v = lane == 0 ? d0 : d1;
+                if (a.bias[0] != nullptr) {
+                    v = v + T::load(a.bias[0][r]);
+                }
+                if (a.residual != nullptr) {
+                    v = T::load(a.residual[r]) + T::load(T::store(v));
+                }
+                a.out[0][r] = T::store(v);
+            }
+        } else if constexpr (MODE == RowMode::kSwiGlu) {
+            if (lane == 0) {
+                a.out[0][cur.r0] = T::store(silu_fixed(d0) * d1);
+            }
+        } else {
+            if (lane == 0) {
+                const int m = cur.m0;
+                const float v0 = d0 + T::load(a.bias[m][cur.r0]);
+                const float v1 = d1 + T::load(a.bias[m][cur.r1]);
+                if constexpr (MODE == RowMode::kQkv) {
+                    a.out[m][cur.r0] = T::store(v0);
+                    a.out[m][cur.r1] = T::store(v1);
+                } else {
+                    float o0 = v0, o1 = v1;
+                    if (m < 2) {
+                        const int64_t d = cur.r0 & 127;
+                        const float c = a.rope_cos[pos * 64 + d];
+                        const float s = a.rope_sin[pos * 64 + d];
+                        o0 = (v0 * c) - (v1 * s);
+                        o1 = (v1 * c) + (v0 * s);
+                    }
+                    if (m == 0) {
+                        a.out[0][cur.r0] = T::store(o0);
+                        a.out[0][cur.r1] = T::store(o1);
+                    } else {
+                        uint16_t* cache = m == 1 ? a.kcache : a.vcache;
+                        const int64_t g = cur.r0 >> 7;
+                        const int64_t base = (g * a.capacity + pos) * 128;
+                        cache[base + (cur.r0 & 127)] = T::store(o0);
+                        cache[base + (cur.r1 & 127)] = T::store(o1);
+                    }
+                }
+            }
+        }
+
+        task = next;
+        cur = nxt;
+        pk0 = npk0;
+        pk1 = npk1;
+        am0 = nam0;
+        am1 = nam1;
+    }
+}
+
+template <typename T, int NCHUNK, int R>
+__global__ __launch_bounds__(64 * ((NCHUNK + 63) / 64)) void nf4_down_kernel(Nf4DownArgs a) {
+    constexpr int W = (NCHUNK + 63) / 64;
+    __shared__ float cb[16];
+    __shared__ float red[R][W];
+    load_codebook_lds(cb);
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int c = wave * 64 + lane;
+    const bool valid = c < NCHUNK;
+    float xv[32];
+    if (valid) {
+        const uint4* src = reinterpret_cast<const uint4*>(a.x + static_cast<int64_t>(c) * 32);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            unpack8<T>(src[i], xv + 8 * i);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            xv[j] = 0.0f;
+        }
+    }
+    __syncthreads();
+    const int64_t row_bytes = static_cast<int64_t>(NCHUNK) * 16;
+    const int64_t row_blocks = NCHUNK / 2;
+    for (int64_t rbase = static_cast<int64_t>(blockIdx.x) * R; rbase < a.rows;
+         rbase += static_cast<int64_t>(gridDim.x) * R) {
+        uint4 pk[R];
+        float am[R];
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const int64_t r = rbase + i;
+            if (valid && r < a.rows) {
+                pk[i] = reinterpret_cast<const uint4*>(a.w + r * row_bytes)[c];
+                am[i] = a.absmax[r * row_blocks + (c >> 1)];
+            } else {
+                pk[i] = make_uint4(0, 0, 0, 0);
+                am[i] = 0.0f;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const int64_t r = rbase + i;
+            float p = 0.0f;
+            if (valid && r < a.rows) {
+                p = nf4_chunk_dot_raw(pk[i], xv, cb) * am[i];
+            }
+            p = wave_sum(p);
+            if (lane == 0) {
+                red[i][wave] = p;
+            }
+        }
+        __syncthreads();
+        if (threadIdx.x < R) {
+            const int64_t r = rbase + threadIdx.x;
+            if (r < a.rows) {
+                float s = red[threadIdx.x][0];
+#pragma unroll
+                for (int w = 1; w < W; ++w) {
+                    s = s + red[threadIdx.x][w];
+                }
+                if (a.residual != nullptr) {
+                    s = T::load(a.residual[r]) + T::load(T::store(s));
+                }
+                a.out[r] = T::store(s);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+struct SrcF32 {
+    static __device__ __forceinline__ float load(const float* p, int64_t i) { return p[i]; }
+};
+struct SrcBf16 {
+    static __device__ __forceinline__ float load(const uint16_t* p, int64_t i) { return bf16_to_f32(p[i]); }
+};
+
+// One wave per 64-element block: absmax by a max-butterfly (order free),
+// scale by the reciprocal, pick the code by counting decision points.
+template <typename S, typename P>
+__global__ __launch_bounds__(256) void nf4_quantize_kernel(const P* src, int64_t nblocks, uint8_t* packed,
+                                                           float* absmax) {
+    const int lane = threadIdx.x & 63;
+    const int64_t blk = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (blk >= nblocks) {
+        return;
+    }
+    const float v = S::load(src, blk * 64 + lane);
+    float m = fabsf(v);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        m = fmaxf(m, __shfl_xor(m, o, 64));
+    }
+    int code = 7;
+    if (m > 0.0f) {
+        const float s = v * (1.0f / m);
+        code = 0;
+#pragma unroll
+        for (int i = 0; i < 15; ++i) {
+            code += s > kNf4Mid[i] ? 1 : 0;
+        }
+    }
+    const int partner = __shfl_xor(code, 1, 64);
+    if ((lane & 1) == 0) {
+        packed[blk * 32 + (lane >> 1)] = static_cast<uint8_t>((code << 4) | partner);
+    }
+    if (lane == 0) {
+        absmax[blk] = m;
+    }
+}
+
+__global__ __launch_bounds__(256) void nf4_dequantize_kernel(const uint8_t* packed, const float* absmax, int64_t n,
+                                                             int64_t blocksize, int out_kind, void* out) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= n) {
+        return;
+    }
+    const uint32_t byte = packed[i >> 1];
+    const uint32_t code = (i & 1) == 0 ? (byte >> 4) : (byte & 0xfu);
+    const float v = kNf4Codebook[code] * absmax[i / blocksize];
+    if (out_kind == 0) {
+        static_cast<float*>(out)[i] = v;
+    } else if (out_kind == 1) {
+        static_cast<uint16_t*>(out)[i] = f32_to_bf16(v);
+    } else {
+        static_cast<uint16_t*>(out)[i] = f32_to_f16(v);
+    }
+}
+
+template <typename T, RowMode MODE>
+hipError_t launch_rows_t(const Nf4RowsArgs& a, hipStream_t stream) {
+    int64_t ntasks = 0;
+    if (MODE == RowMode::kGemv) {
+        ntasks = (a.rows[0] + 1) / 2;
+    } else if (MODE == RowMode::kSwiGlu) {
+        ntasks = a.rows[0];
+    } else {
+        ntasks = (a.rows[0] + a.rows[1] + a.rows[2]) / 2;
+    }
+    if (ntasks <= 0) {
+        return hipSuccess;
+    }
+    const int64_t waves_per_block = kRowsThreads / 64;
+    int64_t blocks = (ntasks + waves_per_block - 1) / waves_per_block;
+    const int64_t max_blocks = 512;  // 2048 waves: 8 per CU on 256 CUs
+    if (blocks > max_blocks) {
+        blocks = max_blocks;
+    }
+    hipLaunchKernelGGL((nf4_rows2048_kernel<T, MODE>), dim3(static_cast<unsigned>(blocks)), dim3(kRowsThreads), 0,
+                       stream, a, ntasks);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_rows_mode(RowMode mode, const Nf4RowsArgs& a, hipStream_t stream) {
+    switch (mode) {
+        case RowMode::kGemv:
+            return launch_rows_t<T, RowMode::kGemv>(a, stream);
+        case RowMode::kQkv:
+            return launch_rows_t<T, RowMode::kQkv>(a, stream);
+        case RowMode::kQkvRope:
+            return launch_rows_t<T, RowMode::kQkvRope>(a, stream);
+        case RowMode::kSwiGlu:
+            return launch_rows_t<T, RowMode::kSwiGlu>(a, stream);
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+hipError_t launch_nf4_rows2048(RowMode mode, Act act, const Nf4RowsArgs& a, hipStream_t stream) {
+    return act == Act::kBf16 ? launch_rows_mode<Bf16>(mode, a, stream) : launch_rows_mode<F16>(mode, a, stream);
+}
+
+hipError_t launch_nf4_down11008(Act act, const Nf4DownArgs& a, hipStream_t stream) {
+    constexpr int kChunks = 11008 / 32;
+    constexpr int kRows = 4;
+    constexpr int kThreads = 64 * ((kChunks + 63) / 64);
+    if (a.rows <= 0) {
+        return hipSuccess;
+    }
+    const int64_t blocks = (a.rows + kRows - 1) / kRows;
+    if (act == Act::kBf16) {
+        hipLaunchKernelGGL((nf4_down_kernel<Bf16, kChunks, kRows>), dim3(static_cast<unsigned>(blocks)),
+                           dim3(kThreads), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL((nf4_down_kernel<F16, kChunks, kRows>), dim3(static_cast<unsigned>(blocks)),
+                           dim3(kThreads), 0, stream, a);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_nf4_quantize_f32(const float* src, int64_t n, uint8_t* packed, float* absmax, hipStream_t stream) {
+    const int64_t nblocks = n / 64;
+    if (nblocks <= 0) {
+        return hipSuccess;
+    }
+    hipLaunchKernelGGL((nf4_quantize_kernel<SrcF32, float>), dim3(static_cast<unsigned>((nblocks + 3) / 4)),
+                       dim3(256), 0, stream, src, nblocks, packed, absmax);
+    return hipGetLastError();
+}
+
+hipError_t launch_nf4_quantize_bf16(const uint16_t* src, int64_t n, uint8_t* packed, float* absmax,
+                                    hipStream_t stream) {
+    const int64_t nblocks = n / 64;
+    if (nblocks <= 0) {
+        return hipSuccess;
+    }
+    hipLaunchKernelGGL((nf4_quantize_kernel<SrcBf16, uint16_t>), dim3(static_cast<unsigned>((nblocks + 3) / 4)),
+                       dim3(256), 0, stream, src, nblocks, packed, absmax);
+    return hipGetLastError();
+}
+
+hipError_t launch_nf4_dequantize(const uint8_t* packed, const float* absmax, int64_t n, int64_t blocksize,
+                                 int out_kind, void* out, hipStream_t stream) {
+    if (n <= 0) {
+        return hipSuccess;
+    }
+    hipLaunchKernelGGL(nf4_dequantize_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream,
+                       packed, absmax, n, blocksize, out_kind, out);
+    return hipGetLastError();
+}
+
+}  // namespace kc

@@ -1,0 +1,1178 @@
+// Host side of libkudacuda.so: the C ABI declared in include/kudacuda.h.
+//
+// Handle lifecycle, error text and the exact-shape guards follow the
+// reference runtime (runtime/kudacuda_runtime.cu:228-1226): status 0/1,
+// per-handle last_error, "called before kudacuda_freeze" and non-null checks,
+// no synchronisation on the launch path, launch errors taken from
+// hipGetLastError.  Unlike the reference, every NF4 QKV version and every GQA
+// variant maps onto one gfx950 kernel family (kc_nf4.hip, kc_gqa.hip).
+#include <hip/hip_runtime.h>
+
+#include <array>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/kudacuda.h"
+#include "kc_device.h"
+#include "kc_kernels.h"
+
+namespace kc {
+namespace {
+
+constexpr int64_t kMaxStandaloneKv = 65536;
+constexpr int64_t kMaxModelKv = 32768;
+
+struct Handle {
+    explicit Handle(int id) : device_id(id) {}
+    ~Handle() {
+        if (graph_exec != nullptr) {
+            (void)hipGraphExecDestroy(graph_exec);
+        }
+        if (graph != nullptr) {
+            (void)hipGraphDestroy(graph);
+        }
+        if (scratch != nullptr) {
+            (void)hipFree(scratch);
+        }
+    }
+    void set_error(const std::string& message) { last_error = message; }
+    void set_hip_error(const char* operation, hipError_t status) {
+        last_error = std::string(operation) + ": " + hipGetErrorString(status);
+    }
+
+    int device_id;
+    bool device_ready = false;
+    bool frozen = false;
+    bool capturing = false;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t graph_exec = nullptr;
+    std::string last_error;
+    // fixed scratch for the standalone attention / argmax entry points
+    void* scratch = nullptr;
+    float* gqa_partials = nullptr;
+    float* lm_best = nullptr;
+    uint32_t* counters = nullptr;  // [0..1] attention, [2] lm_head
+    int32_t* argmax_slot = nullptr;
+};
+
+Handle* as_handle(void* raw) { return reinterpret_cast<Handle*>(raw); }
+
+template <typename T>
+T* ptr(uint64_t v) {
+    return reinterpret_cast<T*>(static_cast<uintptr_t>(v));
+}
+
+hipStream_t as_stream(uint64_t v) { return reinterpret_cast<hipStream_t>(static_cast<uintptr_t>(v)); }
+
+// Shared prologue: valid handle, frozen.
+bool ready(Handle* h, const char* symbol) {
+    if (h == nullptr) {
+        return false;
+    }
+    if (!h->frozen) {
+        h->set_error(std::string(symbol) + " called before kudacuda_freeze");
+        return false;
+    }
+    return true;
+}
+
+int finish(Handle* h, const char* operation, hipError_t status) {
+    if (status != hipSuccess) {
+        h->set_hip_error(operation, status);
+        return 1;
+    }
+    h->last_error.clear();
+    return 0;
+}
+
+int64_t gqa_splits(int64_t tokens) {
+    const int64_t chunk = gqa_chunk_for(tokens);
+    return (tokens + chunk - 1) / chunk;
+}
+
+int64_t gqa_workspace(int64_t tokens) { return 16 * gqa_splits(tokens) * 130; }
+
+const char* const kGfx950Tactics[] = {
+    "qwen2_gqa_decode_gfx950_fp16",
+    "qwen2_gqa_decode_gfx950_bf16",
+    "qwen2_gqa_decode_gfx950_fp16_graph_v1",
+    "qwen2_gqa_decode_gfx950_bf16_graph_v1",
+    "qwen2_gqa_decode_gfx950_fp16_group_tiled_v2",
+    "qwen2_gqa_decode_gfx950_fp16_vectorized_v2",
+    "qwen2_gqa_decode_gfx950_fp16_workspace_v3",
+    "qwen2_gqa_decode_sm86_fp16",
+    "qwen2_gqa_decode_sm89_fp16",
+    "qwen2_gqa_decode_sm86_fp16_group_tiled_v2",
+    "qwen2_gqa_decode_sm89_fp16_group_tiled_v2",
+    "qwen2_gqa_decode_sm86_fp16_vectorized_v2",
+    "qwen2_gqa_decode_sm89_fp16_vectorized_v2",
+    "qwen2_gqa_decode_sm86_fp16_graph_v1",
+    "qwen2_gqa_decode_sm89_fp16_graph_v1",
+};
+
+// ------------------------------------------------------------- NF4 QKV
+int qkv_common(void* raw, const char* symbol, Act act, uint64_t input, uint64_t norm_weight, uint64_t qw,
+               uint64_t qa, uint64_t qb, uint64_t kw, uint64_t ka, uint64_t kb, uint64_t vw, uint64_t va, uint64_t vb,
+               uint64_t normalized, bool need_normalized, uint64_t qo, uint64_t ko, uint64_t vo, int64_t rows,
+               int64_t hidden, int64_t q_out, int64_t kv_out, int64_t blocksize, float epsilon, uint64_t stream) {
+    Handle* h = as_handle(raw);
+    const std::string name = std::string("kudacuda_") + symbol;
+    if (!ready(h, name.c_str())) {
+        return 1;
+    }
+    if (input == 0 || norm_weight == 0 || qw == 0 || qa == 0 || qb == 0 || kw == 0 || ka == 0 || kb == 0 || vw == 0 ||
+        va == 0 || vb == 0 || qo == 0 || ko == 0 || vo == 0 || (need_normalized && normalized == 0)) {
+        h->set_error(std::string(symbol) + " requires non-null device pointers");
+        return 1;
+    }
+    if (rows != 1 || hidden != 2048 || q_out != 2048 || kv_out != 256 || blocksize != 64 || !(epsilon > 0.0f)) {
+        h->set_error(std::string(symbol) +
+                     " requires rows=1, hidden=2048, q_out=2048, kv_out=256, blocksize=64, and positive epsilon");
+        return 1;
+    }
+    Nf4RowsArgs a;
+    a.x = ptr<const uint16_t>(input);
+    a.gamma = ptr<const uint16_t>(norm_weight);
+    a.eps = epsilon;
+    a.w[0] = ptr<const uint8_t>(qw);
+    a.w[1] = ptr<const uint8_t>(kw);
+    a.w[2] = ptr<const uint8_t>(vw);
+    a.absmax[0] = ptr<const float>(qa);
+    a.absmax[1] = ptr<const float>(ka);
+    a.absmax[2] = ptr<const float>(va);
+    a.bias[0] = ptr<const uint16_t>(qb);
+    a.bias[1] = ptr<const uint16_t>(kb);
+    a.bias[2] = ptr<const uint16_t>(vb);
+    a.out[0] = ptr<uint16_t>(qo);
+    a.out[1] = ptr<uint16_t>(ko);
+    a.out[2] = ptr<uint16_t>(vo);
+    a.rows[0] = q_out;
+    a.rows[1] = kv_out;
+    a.rows[2] = kv_out;
+    a.norm_out = ptr<float>(normalized);
+    return finish(h, symbol, launch_nf4_rows2048(RowMode::kQkv, act, a, as_stream(stream)));
+}
+
+int swiglu_common(void* raw, const char* symbol, Act act, uint64_t input, uint64_t norm_weight, uint64_t gw,
+                  uint64_t ga, uint64_t uw, uint64_t ua, uint64_t output, int64_t rows, int64_t hidden,
+                  int64_t intermediate, int64_t blocksize, float epsilon, uint64_t stream, bool clear_error) {
+    Handle* h = as_handle(raw);
+    const std::string name = std::string("kudacuda_") + symbol;
+    if (!ready(h, name.c_str())) {
+        return 1;
+    }
+    if (input == 0 || norm_weight == 0 || gw == 0 || ga == 0 || uw == 0 || ua == 0 || output == 0) {
+        h->set_error(std::string(symbol) + " requires non-null device pointers");
+        return 1;
+    }
+    if (rows != 1 || hidden != 2048 || intermediate != 11008 || blocksize != 64 || !(epsilon > 0.0f)) {
+        h->set_error(std::string(symbol) +
+                     " requires rows=1, hidden=2048, intermediate=11008, blocksize=64, and positive epsilon");
+        return 1;
+    }
+    Nf4RowsArgs a;
+    a.x = ptr<const uint16_t>(input);
+    a.gamma = ptr<const uint16_t>(norm_weight);
+    a.eps = epsilon;
+    a.w[0] = ptr<const uint8_t>(gw);
+    a.w[1] = ptr<const uint8_t>(uw);
+    a.absmax[0] = ptr<const float>(ga);
+    a.absmax[1] = ptr<const float>(ua);
+    a.out[0] = ptr<uint16_t>(output);
+    a.rows[0] = intermediate;
+    a.rows[1] = intermediate;
+    const hipError_t status = launch_nf4_rows2048(RowMode::kSwiGlu, act, a, as_stream(stream));
+    if (status != hipSuccess) {
+        h->set_hip_error(symbol, status);
+        return 1;
+    }
+    if (clear_error) {
+        h->last_error.clear();
+    }
+    return 0;
+}
+
+// ------------------------------------------------------------------ GQA
+struct GqaShape {
+    int64_t batch, query_len, query_heads, kv_heads, head_dim;
+    float scale;
+};
+
+bool gqa_shape_ok(Handle* h, const char* symbol, const GqaShape& s, const char* len_name, int64_t len,
+                  int64_t len_max) {
+    if (s.batch != 1 || s.query_len != 1 || len < 1 || len > len_max || s.query_heads != 16 || s.kv_heads != 2 ||
+        s.head_dim != 128) {
+        h->set_error(std::string(symbol) + " requires batch=1, query_len=1, " + len_name + "=1.." +
+                     std::to_string(len_max) + ", q_heads=16, kv_heads=2, head_dim=128");
+        return false;
+    }
+    if (!(s.scale > 0.0f)) {
+        h->set_error(std::string(symbol) + " scale must be positive");
+        return false;
+    }
+    return true;
+}
+
+int gqa_direct(void* raw, const char* symbol, Act act, uint64_t q, uint64_t k, uint64_t v, uint64_t out,
+               const GqaShape& s, int64_t kv_len, uint64_t stream) {
+    Handle* h = as_handle(raw);
+    const std::string name = std::string("kudacuda_") + symbol;
+    if (!ready(h, name.c_str())) {
+        return 1;
+    }
+    if (q == 0 || k == 0 || v == 0 || out == 0) {
+        h->set_error(std::string(symbol) + " requires non-null device pointers");
+        return 1;
+    }
+    if (!gqa_shape_ok(h, symbol, s, "kv_len", kv_len, kMaxStandaloneKv)) {
+        return 1;
+    }
+    GqaArgs a;
+    a.q = ptr<const uint16_t>(q);
+    a.k = ptr<const uint16_t>(k);
+    a.v = ptr<const uint16_t>(v);
+    a.out = ptr<uint16_t>(out);
+    a.partials = h->gqa_partials;
+    a.counters = h->counters;
+    a.kv_len_host = kv_len;
+    a.capacity = kv_len;
+    a.chunk = gqa_chunk_for(kv_len);
+    a.max_splits = gqa_splits(kv_len);
+    a.qk_scale_log2 = s.scale * kLog2e;
+    return finish(h, symbol, launch_gqa_decode(act, a, as_stream(stream)));
+}
+
+int gqa_graph(void* raw, const char* symbol, Act act, uint64_t q, uint64_t k, uint64_t v, uint64_t out,
+              const GqaShape& s, int64_t kv_capacity, uint64_t kv_len_device, uint64_t stream) {
+    Handle* h = as_handle(raw);
+    const std::string name = std::string("kudacuda_") + symbol;
+    if (!ready(h, name.c_str())) {
+        return 1;
+    }
+    if (q == 0 || k == 0 || v == 0 || out == 0 || kv_len_device == 0) {
+        h->set_error(std::string(symbol) + " requires non-null device pointers");
+        return 1;
+    }
+    if (!gqa_shape_ok(h, symbol, s, "kv_capacity", kv_capacity, kMaxStandaloneKv)) {
+        return 1;
+    }
+    GqaArgs a;
+    a.q = ptr<const uint16_t>(q);
+    a.k = ptr<const uint16_t>(k);
+    a.v = ptr<const uint16_t>(v);
+    a.out = ptr<uint16_t>(out);
+    a.partials = h->gqa_partials;
+    a.counters = h->counters;
+    a.kv_len_device = ptr<const int32_t>(kv_len_device);
+    a.capacity = kv_capacity;
+    a.chunk = gqa_chunk_for(kv_capacity);
+    a.max_splits = gqa_splits(kv_capacity);
+    a.qk_scale_log2 = s.scale * kLog2e;
+    return finish(h, symbol, launch_gqa_decode(act, a, as_stream(stream)));
+}
+
+// ---------------------------------------------------------------- model
+struct Model {
+    Handle* handle = nullptr;
+    int64_t num_layers = 0;
+    int64_t vocab = 0;
+    int64_t capacity = 0;
+    float eps = 1e-6f;
+    std::vector<std::array<uint64_t, KUDACUDA_QWEN2_LAYER_FIELDS>> layers;
+    std::array<uint64_t, KUDACUDA_QWEN2_MODEL_FIELDS> g{};
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    ~Model() {
+        if (exec != nullptr) {
+            (void)hipGraphExecDestroy(exec);
+        }
+        if (graph != nullptr) {
+            (void)hipGraphDestroy(graph);
+        }
+    }
+};
+
+hipError_t model_op(const Model& m, int op, int64_t layer, bool bookkeeping, hipStream_t stream) {
+    const auto& L = m.layers[static_cast<size_t>(layer)];
+    const auto& G = m.g;
+    switch (op) {
+        case 0: {
+            Nf4RowsArgs a;
+            a.x = ptr<const uint16_t>(G[KUDACUDA_QWEN2_HIDDEN]);
+            a.gamma = ptr<const uint16_t>(L[KUDACUDA_QWEN2_INPUT_NORM]);
+            a.eps = m.eps;
+            a.w[0] = ptr<const uint8_t>(L[KUDACUDA_QWEN2_Q_PACKED]);
+            a.w[1] = ptr<const uint8_t>(L[KUDACUDA_QWEN2_K_PACKED]);
+            a.w[2] = ptr<const uint8_t>(L[KUDACUDA_QWEN2_V_PACKED]);
+            a.absmax[0] = ptr<const float>(L[KUDACUDA_QWEN2_Q_ABSMAX]);
+            a.absmax[1] = ptr<const float>(L[KUDACUDA_QWEN2_K_ABSMAX]);
+            a.absmax[2] = ptr<const float>(L[KUDACUDA_QWEN2_V_ABSMAX]);
+            a.bias[0] = ptr<const uint16_t>(L[KUDACUDA_QWEN2_Q_BIAS]);
+            a.bias[1] = ptr<const uint16_t>(L[KUDACUDA_QWEN2_K_BIAS]);
+            a.bias[2] = ptr<const uint16_t>(L[KUDACUDA_QWEN2_V_BIAS]);
+            a.out[0] = ptr<uint16_t>(G[KUDACUDA_QWEN2_QUERY]);
+            a.rows[0] = 2048;
+            a.rows[1] = 256;
+            a.rows[2] = 256;
+            a.rope_cos = ptr<const float>(G[KUDACUDA_QWEN2_ROPE_COS]);
+            a.rope_sin = ptr<const float>(G[KUDACUDA_QWEN2_ROPE_SIN]);
+            a.control = ptr<const int32_t>(G[KUDACUDA_QWEN2_CONTROL]);
+            a.capacity = m.capacity;
+            a.kcache = ptr<uint16_t>(L[KUDACUDA_QWEN2_KEY_CACHE]);
+            a.vcache = ptr<uint16_t>(L[KUDACUDA_QWEN2_VALUE_CACHE]);
+            if (layer == 0) {
+                a.embed = ptr<const uint16_t>(G[KUDACUDA_QWEN2_EMBED]);
+                a.tokens = ptr<const int32_t>(G[KUDACUDA_QWEN2_TOKENS]);
+                a.vocab = m.vocab;
+                a.hidden_out = ptr<uint16_t>(G[KUDACUDA_QWEN2_HIDDEN]);
+            }
+            return launch_nf4_rows2048(RowMode::kQkvRope, Act::kBf16, a, stream);
+        }
+        case 1: {
+            GqaArgs a;
+            a.q = ptr<const uint16_t>(G[KUDACUDA_QWEN2_QUERY]);
+            a.k = ptr<const uint16_t>(L[KUDACUDA_QWEN2_KEY_CACHE]);
+            a.v = ptr<const uint16_t>(L[KUDACUDA_QWEN2_VALUE_CACHE]);
+            a.out = ptr<uint16_t>(G[KUDACUDA_QWEN2_ATTN]);
+            a.partials = ptr<float>(G[KUDACUDA_QWEN2_ATTN_PARTIALS]);
+            a.counters = ptr<uint32_t>(G[KUDACUDA_QWEN2_ATTN_COUNTERS]);
+            a.kv_len_device = ptr<const int32_t>(G[KUDACUDA_QWEN2_CONTROL]);
+            a.kv_len_offset = 1;
+            a.capacity = m.capacity;
+            a.chunk = gqa_chunk_for(m.capacity);
+            a.max_splits = gqa_splits(m.capacity);
+            a.qk_scale_log2 = static_cast<float>(1.0 / std::sqrt(128.0)) * kLog2e;
+            return launch_gqa_decode(Act::kBf16, a, stream);
+        }
+        case 2: {
+            Nf4RowsArgs a;
+            a.x = ptr<const uint16_t>(G[KUDACUDA_QWEN2_ATTN]);
+            a.w[0] = ptr<const uint8_t>(L[KUDACUDA_QWEN2_O_PACKED]);
+            a.absmax[0] = ptr<const float>(L[KUDACUDA_QWEN2_O_ABSMAX]);
+            a.out[0] = ptr<uint16_t>(G[KUDACUDA_QWEN2_HIDDEN]);
+            a.residual = ptr<const uint16_t>(G[KUDACUDA_QWEN2_HIDDEN]);
+            a.rows[0] = 2048;
+            return launch_nf4_rows2048(RowMode::kGemv, Act::kBf16, a, stream);
+        }
+        case 3: {
+            Nf4RowsArgs a;
+            a.x = ptr<const uint16_t>(G[KUDACUDA_QWEN2_HIDDEN]);
+            a.gamma = ptr<const uint16_t>(L[KUDACUDA_QWEN2_POST_NORM]);
+            a.eps = m.eps;
+            a.w[0] = ptr<const uint8_t>(L[KUDACUDA_QWEN2_GATE_PACKED]);
+            a.w[1] = ptr<const uint8_t>(L[KUDACUDA_QWEN2_UP_PACKED]);
+            a.absmax[0] = ptr<const float>(L[KUDACUDA_QWEN2_GATE_ABSMAX]);
+            a.absmax[1] = ptr<const float>(L[KUDACUDA_QWEN2_UP_ABSMAX]);
+            a.out[0] = ptr<uint16_t>(G[KUDACUDA_QWEN2_MLP]);
+            a.rows[0] = 11008;
+            a.rows[1] = 11008;
+            return launch_nf4_rows2048(RowMode::kSwiGlu, Act::kBf16, a, stream);
+        }
+        case 4: {
+            Nf4DownArgs a;
+            a.x = ptr<const uint16_t>(G[KUDACUDA_QWEN2_MLP]);
+            a.w = ptr<const uint8_t>(L[KUDACUDA_QWEN2_DOWN_PACKED]);
+            a.absmax = ptr<const float>(L[KUDACUDA_QWEN2_DOWN_ABSMAX]);
+            a.residual = ptr<const uint16_t>(G[KUDACUDA_QWEN2_HIDDEN]);
+            a.out = ptr<uint16_t>(G[KUDACUDA_QWEN2_HIDDEN]);
+            a.rows = 2048;
+            return launch_nf4_down11008(Act::kBf16, a, stream);
+        }
+        case 5: {
+            LmHeadArgs a;
+            a.x = ptr<const uint16_t>(G[KUDACUDA_QWEN2_HIDDEN]);
+            a.gamma = ptr<const uint16_t>(G[KUDACUDA_QWEN2_FINAL_NORM]);
+            a.eps = m.eps;
+            a.weight = ptr<const uint16_t>(G[KUDACUDA_QWEN2_EMBED]);
+            a.vocab = m.vocab;
+            a.logits = ptr<uint16_t>(G[KUDACUDA_QWEN2_LOGITS]);
+            a.block_best = ptr<float>(G[KUDACUDA_QWEN2_LM_BEST]);
+            a.counter = ptr<uint32_t>(G[KUDACUDA_QWEN2_LM_COUNTER]);
+            if (bookkeeping) {
+                a.control = ptr<int32_t>(G[KUDACUDA_QWEN2_CONTROL]);
+                a.tokens = ptr<int32_t>(G[KUDACUDA_QWEN2_TOKENS]);
+            }
+            return launch_lm_head_argmax(a, stream);
+        }
+        default:
+            return hipErrorInvalidValue;
+    }
+}
+
+hipError_t model_step(const Model& m, hipStream_t stream) {
+    for (int64_t layer = 0; layer < m.num_layers; ++layer) {
+        for (int op = 0; op < 5; ++op) {
+            const hipError_t status = model_op(m, op, layer, true, stream);
+            if (status != hipSuccess) {
+                return status;
+            }
+        }
+    }
+    return model_op(m, 5, 0, true, stream);
+}
+
+}  // namespace
+}  // namespace kc
+
+using kc::Act;
+using kc::as_handle;
+using kc::as_stream;
+using kc::finish;
+using kc::Handle;
+using kc::ptr;
+using kc::ready;
+
+extern "C" {
+
+void* kudacuda_create(int device_id) {
+    auto* h = new (std::nothrow) Handle(device_id);
+    if (h == nullptr) {
+        return nullptr;
+    }
+    hipError_t status = hipSetDevice(device_id);
+    if (status != hipSuccess) {
+        h->set_hip_error("hipSetDevice", status);
+        return h;
+    }
+    const size_t partial_bytes = static_cast<size_t>(kc::gqa_workspace(kc::kMaxStandaloneKv)) * sizeof(float);
+    const size_t best_bytes = static_cast<size_t>(kc::lm_head_workspace_floats()) * sizeof(float);
+    const size_t counter_bytes = 64;
+    const size_t total = partial_bytes + best_bytes + counter_bytes;
+    status = hipMalloc(&h->scratch, total);
+    if (status != hipSuccess) {
+        h->scratch = nullptr;
+        h->set_hip_error("hipMalloc(handle scratch)", status);
+        return h;
+    }
+    char* base = static_cast<char*>(h->scratch);
+    h->gqa_partials = reinterpret_cast<float*>(base);
+    h->lm_best = reinterpret_cast<float*>(base + partial_bytes);
+    h->counters = reinterpret_cast<uint32_t*>(base + partial_bytes + best_bytes);
+    h->argmax_slot = reinterpret_cast<int32_t*>(base + partial_bytes + best_bytes + 32);
+    status = hipMemset(h->counters, 0, counter_bytes);
+    if (status == hipSuccess) {
+        status = hipDeviceSynchronize();
+    }
+    if (status != hipSuccess) {
+        h->set_hip_error("hipMemset(handle counters)", status);
+        return h;
+    }
+    h->device_ready = true;
+    return h;
+}
+
+int kudacuda_freeze(void* raw) {
+    Handle* h = as_handle(raw);
+    if (h == nullptr) {
+        return 1;
+    }
+    if (!h->device_ready) {
+        if (h->last_error.empty()) {
+            h->set_error("HIP device is not ready");
+        }
+        return 1;
+    }
+    h->frozen = true;
+    h->last_error.clear();
+    return 0;
+}
+
+int kudacuda_can_dispatch(void* raw, const char* tactic_name, int64_t batch_size, int64_t seq_len) {
+    const Handle* h = as_handle(raw);
+    if (h == nullptr || !h->frozen || tactic_name == nullptr || batch_size <= 0 || seq_len <= 0) {
+        return 0;
+    }
+    for (const char* name : kc::kGfx950Tactics) {
+        if (std::strcmp(tactic_name, name) == 0) {
+            return batch_size == 1 && seq_len == 1 ? 1 : 0;
+        }
+    }
+    return std::strcmp(tactic_name, "vector_add") == 0 || std::strcmp(tactic_name, "rmsnorm") == 0 ? 1 : 0;
+}
+
+int kudacuda_vector_add(void* raw, uint64_t a, uint64_t b, uint64_t output, int64_t count, uint64_t stream) {
+    Handle* h = as_handle(raw);
+    if (!ready(h, "kudacuda_vector_add")) {
+        return 1;
+    }
+    if (a == 0 || b == 0 || output == 0) {
+        h->set_error("vector_add requires non-null device pointers");
+        return 1;
+    }
+    if (count <= 0) {
+        h->set_error("vector_add count must be positive");
+        return 1;
+    }
+    return finish(h, "vector_add_kernel",
+                  kc::launch_vector_add(ptr<const float>(a), ptr<const float>(b), ptr<float>(output), count,
+                                        as_stream(stream)));
+}
+
+int kudacuda_rmsnorm(void* raw, uint64_t input, uint64_t weight, uint64_t output, int64_t rows, int64_t hidden,
+                     float epsilon, uint64_t stream) {
+    Handle* h = as_handle(raw);
+    if (!ready(h, "kudacuda_rmsnorm")) {
+        return 1;
+    }
+    if (input == 0 || weight == 0 || output == 0) {
+        h->set_error("rmsnorm requires non-null device pointers");
+        return 1;
+    }
+    if (rows <= 0 || hidden <= 0) {
+        h->set_error("rmsnorm rows and hidden must be positive");
+        return 1;
+    }
+    if (!(epsilon > 0.0f)) {
+        h->set_error("rmsnorm epsilon must be positive");
+        return 1;
+    }
+    return finish(h, "rmsnorm_kernel",
+                  kc::launch_rmsnorm_f32(ptr<const float>(input), ptr<const float>(weight), ptr<float>(output), rows,
+                                         hidden, epsilon, as_stream(stream)));
+}
+
+int kudacuda_fused_rmsnorm_qkv(void* raw, uint64_t input, uint64_t norm_weight, uint64_t qkv_weight, uint64_t bias,
+                               uint64_t output, int64_t rows, int64_t hidden, float epsilon, uint64_t stream) {
+    Handle* h = as_handle(raw);
+    if (!ready(h, "kudacuda_fused_rmsnorm_qkv")) {
+        return 1;
+    }
+    if (input == 0 || norm_weight == 0 || qkv_weight == 0 || output == 0) {
+        h->set_error("fused_rmsnorm_qkv requires non-null input, weights, and output pointers");
+        return 1;
+    }
+    if (rows <= 0 || hidden <= 0 || !(epsilon > 0.0f)) {
+        h->set_error("fused_rmsnorm_qkv requires positive rows, hidden, and epsilon");
+        return 1;
+    }
+    return finish(h, "fused_rmsnorm_qkv_kernel",
+                  kc::launch_dense_rmsnorm_qkv_f16(ptr<const uint16_t>(input), ptr<const uint16_t>(norm_weight),
+                                                   ptr<const uint16_t>(qkv_weight), ptr<const uint16_t>(bias),
+                                                   ptr<uint16_t>(output), rows, hidden, epsilon, as_stream(stream)));
+}
+
+int kudacuda_qwen2_fused_rmsnorm_qkv_nf4(void* raw, uint64_t input, uint64_t norm_weight, uint64_t q_weight_packed,
+                                         uint64_t q_absmax, uint64_t q_bias, uint64_t k_weight_packed,
+                                         uint64_t k_absmax, uint64_t k_bias, uint64_t v_weight_packed,
+                                         uint64_t v_absmax, uint64_t v_bias, uint64_t q_output, uint64_t k_output,
+                                         uint64_t v_output, int64_t rows, int64_t hidden, int64_t q_out,
+                                         int64_t kv_out, int64_t blocksize, float epsilon, uint64_t stream) {
+    return kc::qkv_common(raw, "qwen2_fused_rmsnorm_qkv_nf4", Act::kF16, input, norm_weight, q_weight_packed, q_absmax,
+                          q_bias, k_weight_packed, k_absmax, k_bias, v_weight_packed, v_absmax, v_bias, 0, false,
+                          q_output, k_output, v_output, rows, hidden, q_out, kv_out, blocksize, epsilon, stream);
+}
+
+int kudacuda_qwen2_fused_rmsnorm_qkv_nf4_v2(void* raw, uint64_t input, uint64_t norm_weight,
+                                            uint64_t q_weight_packed, uint64_t q_absmax, uint64_t q_bias,
+                                            uint64_t k_weight_packed, uint64_t k_absmax, uint64_t k_bias,
+                                            uint64_t v_weight_packed, uint64_t v_absmax, uint64_t v_bias,
+                                            uint64_t normalized_workspace, uint64_t q_output, uint64_t k_output,
+                                            uint64_t v_output, int64_t rows, int64_t hidden, int64_t q_out,
+                                            int64_t kv_out, int64_t blocksize, float epsilon, uint64_t stream) {
+    return kc::qkv_common(raw, "qwen2_fused_rmsnorm_qkv_nf4_v2", Act::kF16, input, norm_weight, q_weight_packed,
+                          q_absmax, q_bias, k_weight_packed, k_absmax, k_bias, v_weight_packed, v_absmax, v_bias,
+                          normalized_workspace, true, q_output, k_output, v_output, rows, hidden, q_out, kv_out,
+                          blocksize, epsilon, stream);
+}
+
+int kudacuda_qwen2_fused_rmsnorm_qkv_nf4_v3(void* raw, uint64_t input, uint64_t norm_weight,
+                                            uint64_t q_weight_packed, uint64_t q_absmax, uint64_t q_bias,
+                                            uint64_t k_weight_packed, uint64_t k_absmax, uint64_t k_bias,
+                                            uint64_t v_weight_packed, uint64_t v_absmax, uint64_t v_bias,
+                                            uint64_t normalized_workspace, uint64_t q_output, uint64_t k_output,
+                                            uint64_t v_output, int64_t rows, int64_t hidden, int64_t q_out,
+                                            int64_t kv_out, int64_t blocksize, float epsilon, uint64_t stream) {
+    return kc::qkv_common(raw, "qwen2_fused_rmsnorm_qkv_nf4_v3", Act::kF16, input, norm_weight, q_weight_packed,
+                          q_absmax, q_bias, k_weight_packed, k_absmax, k_bias, v_weight_packed, v_absmax, v_bias,
+                          normalized_workspace, true, q_output, k_output, v_output, rows, hidden, q_out, kv_out,
+                          blocksize, epsilon, stream);
+}
+
+int kudacuda_qwen2_fused_rmsnorm_qkv_nf4_bf16(void* raw, uint64_t input, uint64_t norm_weight,
+                                              uint64_t q_weight_packed, uint64_t q_absmax, uint64_t q_bias,
+                                              uint64_t k_weight_packed, uint64_t k_absmax, uint64_t k_bias,
+                                              uint64_t v_weight_packed, uint64_t v_absmax, uint64_t v_bias,
+                                              uint64_t q_output, uint64_t k_output, uint64_t v_output, int64_t rows,
+                                              int64_t hidden, int64_t q_out, int64_t kv_out, int64_t blocksize,
+                                              float epsilon, uint64_t stream) {
+    return kc::qkv_common(raw, "qwen2_fused_rmsnorm_qkv_nf4_bf16", Act::kBf16, input, norm_weight, q_weight_packed,
+                          q_absmax, q_bias, k_weight_packed, k_absmax, k_bias, v_weight_packed, v_absmax, v_bias, 0,
+                          false, q_output, k_output, v_output, rows, hidden, q_out, kv_out, blocksize, epsilon,
+                          stream);
+}
+
+int kudacuda_qwen2_qkv_rope_cache_nf4_bf16(void* raw, uint64_t input, uint64_t norm_weight, uint64_t q_weight_packed,
+                                           uint64_t q_absmax, uint64_t q_bias, uint64_t k_weight_packed,
+                                           uint64_t k_absmax, uint64_t k_bias, uint64_t v_weight_packed,
+                                           uint64_t v_absmax, uint64_t v_bias, uint64_t rope_cos, uint64_t rope_sin,
+                                           uint64_t position_device, uint64_t q_output, uint64_t key_cache,
+                                           uint64_t value_cache, int64_t kv_capacity, int64_t hidden, int64_t q_out,
+                                           int64_t kv_out, int64_t blocksize, float epsilon, uint64_t stream) {
+    Handle* h = as_handle(raw);
+    const char* symbol = "qwen2_qkv_rope_cache_nf4_bf16";
+    if (!ready(h, "kudacuda_qwen2_qkv_rope_cache_nf4_bf16")) {
+        return 1;
+    }
+    if (input == 0 || norm_weight == 0 || q_weight_packed == 0 || q_absmax == 0 || q_bias == 0 ||
+        k_weight_packed == 0 || k_absmax == 0 || k_bias == 0 || v_weight_packed == 0 || v_absmax == 0 ||
+        v_bias == 0 || rope_cos == 0 || rope_sin == 0 || position_device == 0 || q_output == 0 || key_cache == 0 ||
+        value_cache == 0) {
+        h->set_error(std::string(symbol) + " requires non-null device pointers");
+        return 1;
+    }
+    if (hidden != 2048 || q_out != 2048 || kv_out != 256 || blocksize != 64 || kv_capacity < 1 ||
+        kv_capacity > kc::kMaxModelKv || !(epsilon > 0.0f)) {
+        h->set_error(std::string(symbol) +
+                     " requires hidden=2048, q_out=2048, kv_out=256, blocksize=64, kv_capacity=1..32768, and "
+                     "positive epsilon");
+        return 1;
+    }
+    kc::Nf4RowsArgs a;
+    a.x = ptr<const uint16_t>(input);
+    a.gamma = ptr<const uint16_t>(norm_weight);
+    a.eps = epsilon;
+    a.w[0] = ptr<const uint8_t>(q_weight_packed);
+    a.w[1] = ptr<const uint8_t>(k_weight_packed);
+    a.w[2] = ptr<const uint8_t>(v_weight_packed);
+    a.absmax[0] = ptr<const float>(q_absmax);
+    a.absmax[1] = ptr<const float>(k_absmax);
+    a.absmax[2] = ptr<const float>(v_absmax);
+    a.bias[0] = ptr<const uint16_t>(q_bias);
+    a.bias[1] = ptr<const uint16_t>(k_bias);
+    a.bias[2] = ptr<const uint16_t>(v_bias);
+    a.out[0] = ptr<uint16_t>(q_output);
+    a.rows[0] = 2048;
+    a.rows[1] = 256;
+    a.rows[2] = 256;
+    a.rope_cos = ptr<const float>(rope_cos);
+    a.rope_sin = ptr<const float>(rope_sin);
+    a.control = ptr<const int32_t>(position_device);
+    a.capacity = kv_capacity;
+    a.kcache = ptr<uint16_t>(key_cache);
+    a.vcache = ptr<uint16_t>(value_cache);
+    return finish(h, symbol, kc::launch_nf4_rows2048(kc::RowMode::kQkvRope, Act::kBf16, a, as_stream(stream)));
+}
+
+int kudacuda_qwen2_swiglu_nf4(void* raw, uint64_t input, uint64_t norm_weight, uint64_t gate_weight_packed,
+                              uint64_t gate_absmax, uint64_t up_weight_packed, uint64_t up_absmax, uint64_t output,
+                              int64_t rows, int64_t hidden, int64_t intermediate, int64_t blocksize, float epsilon,
+                              uint64_t stream) {
+    // The reference leaves last_error untouched on success for this symbol
+    // (runtime/kudacuda_runtime.cu:750); kept.
+    return kc::swiglu_common(raw, "qwen2_swiglu_nf4", Act::kF16, input, norm_weight, gate_weight_packed, gate_absmax,
+                             up_weight_packed, up_absmax, output, rows, hidden, intermediate, blocksize, epsilon,
+                             stream, false);
+}
+
+int kudacuda_qwen2_swiglu_nf4_bf16(void* raw, uint64_t input, uint64_t norm_weight, uint64_t gate_weight_packed,
+                                   uint64_t gate_absmax, uint64_t up_weight_packed, uint64_t up_absmax,
+                                   uint64_t output, int64_t rows, int64_t hidden, int64_t intermediate,
+                                   int64_t blocksize, float epsilon, uint64_t stream) {
+    return kc::swiglu_common(raw, "qwen2_swiglu_nf4_bf16", Act::kBf16, input, norm_weight, gate_weight_packed,
+                             gate_absmax, up_weight_packed, up_absmax, output, rows, hidden, intermediate, blocksize,
+                             epsilon, stream, true);
+}
+
+int kudacuda_qwen2_mlp_nf4_bf16(void* raw, uint64_t input, uint64_t norm_weight, uint64_t gate_weight_packed,
+                                uint64_t gate_absmax, uint64_t up_weight_packed, uint64_t up_absmax,
+                                uint64_t down_weight_packed, uint64_t down_absmax, uint64_t intermediate_workspace,
+                                uint64_t residual, uint64_t output, int64_t rows, int64_t hidden,
+                                int64_t intermediate, int64_t blocksize, float epsilon, uint64_t stream) {
+    Handle* h = as_handle(raw);
+    const char* symbol = "qwen2_mlp_nf4_bf16";
+    if (!ready(h, "kudacuda_qwen2_mlp_nf4_bf16")) {
+        return 1;
+    }
+    if (input == 0 || gate_weight_packed == 0 || gate_absmax == 0 || up_weight_packed == 0 || up_absmax == 0 ||
+        down_weight_packed == 0 || down_absmax == 0 || intermediate_workspace == 0 || output == 0) {
+        h->set_error(std::string(symbol) + " requires non-null device pointers");
+        return 1;
+    }
+    if (rows != 1 || hidden != 2048 || intermediate != 11008 || blocksize != 64 ||
+        (norm_weight != 0 && !(epsilon > 0.0f))) {
+        h->set_error(std::string(symbol) +
+                     " requires rows=1, hidden=2048, intermediate=11008, blocksize=64, and positive epsilon");
+        return 1;
+    }
+    kc::Nf4RowsArgs a;
+    a.x = ptr<const uint16_t>(input);
+    a.gamma = ptr<const uint16_t>(norm_weight);
+    a.eps = epsilon;
+    a.w[0] = ptr<const uint8_t>(gate_weight_packed);
+    a.w[1] = ptr<const uint8_t>(up_weight_packed);
+    a.absmax[0] = ptr<const float>(gate_absmax);
+    a.absmax[1] = ptr<const float>(up_absmax);
+    a.out[0] = ptr<uint16_t>(intermediate_workspace);
+    a.rows[0] = intermediate;
+    a.rows[1] = intermediate;
+    hipError_t status = kc::launch_nf4_rows2048(kc::RowMode::kSwiGlu, Act::kBf16, a, as_stream(stream));
+    if (status != hipSuccess) {
+        return finish(h, "qwen2_mlp_nf4_bf16(gate_up)", status);
+    }
+    kc::Nf4DownArgs d;
+    d.x = ptr<const uint16_t>(intermediate_workspace);
+    d.w = ptr<const uint8_t>(down_weight_packed);
+    d.absmax = ptr<const float>(down_absmax);
+    d.residual = ptr<const uint16_t>(residual);
+    d.out = ptr<uint16_t>(output);
+    d.rows = hidden;
+    return finish(h, "qwen2_mlp_nf4_bf16(down)", kc::launch_nf4_down11008(Act::kBf16, d, as_stream(stream)));
+}
+
+int kudacuda_nf4_gemv_bf16(void* raw, uint64_t input, uint64_t weight_packed, uint64_t absmax, uint64_t bias,
+                           uint64_t residual, uint64_t output, int64_t rows, int64_t in_features,
+                           int64_t out_features, int64_t blocksize, uint64_t stream) {
+    Handle* h = as_handle(raw);
+    const char* symbol = "nf4_gemv_bf16";
+    if (!ready(h, "kudacuda_nf4_gemv_bf16")) {
+        return 1;
+    }
+    if (input == 0 || weight_packed == 0 || absmax == 0 || output == 0) {
+        h->set_error(std::string(symbol) + " requires non-null device pointers");
+        return 1;
+    }
+    if (rows != 1 || in_features != 2048 || out_features < 1 || blocksize != 64) {
+        h->set_error(std::string(symbol) + " requires rows=1, in_features=2048, out_features>=1, blocksize=64");
+        return 1;
+    }
+    kc::Nf4RowsArgs a;
+    a.x = ptr<const uint16_t>(input);
+    a.w[0] = ptr<const uint8_t>(weight_packed);
+    a.absmax[0] = ptr<const float>(absmax);
+    a.bias[0] = ptr<const uint16_t>(bias);
+    a.residual = ptr<const uint16_t>(residual);
+    a.out[0] = ptr<uint16_t>(output);
+    a.rows[0] = out_features;
+    return finish(h, symbol, kc::launch_nf4_rows2048(kc::RowMode::kGemv, Act::kBf16, a, as_stream(stream)));
+}
+
+int kudacuda_nf4_quantize(void* raw, uint64_t input, int64_t input_dtype, int64_t count, int64_t blocksize,
+                          uint64_t packed_output, uint64_t absmax_output, uint64_t stream) {
+    Handle* h = as_handle(raw);
+    const char* symbol = "nf4_quantize";
+    if (!ready(h, "kudacuda_nf4_quantize")) {
+        return 1;
+    }
+    if (input == 0 || packed_output == 0 || absmax_output == 0) {
+        h->set_error(std::string(symbol) + " requires non-null device pointers");
+        return 1;
+    }
+    if (blocksize != 64 || count <= 0 || count % 64 != 0 || (input_dtype != 0 && input_dtype != 1)) {
+        h->set_error(std::string(symbol) +
+                     " requires blocksize=64, a positive count divisible by 64, and input_dtype 0 (fp32) or 1 (bf16)");
+        return 1;
+    }
+    const hipError_t status =
+        input_dtype == 0
+            ? kc::launch_nf4_quantize_f32(ptr<const float>(input), count, ptr<uint8_t>(packed_output),
+                                          ptr<float>(absmax_output), as_stream(stream))
+            : kc::launch_nf4_quantize_bf16(ptr<const uint16_t>(input), count, ptr<uint8_t>(packed_output),
+                                           ptr<float>(absmax_output), as_stream(stream));
+    return finish(h, symbol, status);
+}
+
+int kudacuda_nf4_dequantize(void* raw, uint64_t packed, uint64_t absmax, int64_t count, int64_t blocksize,
+                            int64_t output_dtype, uint64_t output, uint64_t stream) {
+    Handle* h = as_handle(raw);
+    const char* symbol = "nf4_dequantize";
+    if (!ready(h, "kudacuda_nf4_dequantize")) {
+        return 1;
+    }
+    if (packed == 0 || absmax == 0 || output == 0) {
+        h->set_error(std::string(symbol) + " requires non-null device pointers");
+        return 1;
+    }
+    if (blocksize <= 0 || count <= 0 || output_dtype < 0 || output_dtype > 2) {
+        h->set_error(std::string(symbol) + " requires positive count and blocksize and output_dtype 0, 1 or 2");
+        return 1;
+    }
+    return finish(h, symbol,
+                  kc::launch_nf4_dequantize(ptr<const uint8_t>(packed), ptr<const float>(absmax), count, blocksize,
+                                            static_cast<int>(output_dtype), ptr<void>(output), as_stream(stream)));
+}
+
+int kudacuda_qwen2_gqa_decode_workspace_v3(void* raw, uint64_t query, uint64_t key_cache, uint64_t value_cache,
+                                           uint64_t output, uint64_t workspace, uint64_t kv_len_device,
+                                           int64_t batch_size, int64_t query_len, int64_t kv_capacity,
+                                           int64_t query_heads, int64_t kv_heads, int64_t head_dim, float scale,
+                                           uint64_t stream) {
+    Handle* h = as_handle(raw);
+    const char* symbol = "qwen2_gqa_decode_workspace_v3";
+    if (!ready(h, "kudacuda_qwen2_gqa_decode_workspace_v3")) {
+        return 1;
+    }
+    if (query == 0 || key_cache == 0 || value_cache == 0 || output == 0 || workspace == 0 || kv_len_device == 0) {
+        h->set_error(std::string(symbol) + " requires non-null device pointers");
+        return 1;
+    }
+    if (batch_size != 1 || query_len != 1 || kv_capacity < 1 || kv_capacity > 512 || query_heads != 16 ||
+        kv_heads != 2 || head_dim != 128 || !(scale > 0.0f)) {
+        h->set_error(std::string(symbol) +
+                     " requires 1x1, capacity=1..512, heads=16/2, head_dim=128, and positive scale");
+        return 1;
+    }
+    kc::GqaArgs a;
+    a.q = ptr<const uint16_t>(query);
+    a.k = ptr<const uint16_t>(key_cache);
+    a.v = ptr<const uint16_t>(value_cache);
+    a.out = ptr<uint16_t>(output);
+    a.partials = ptr<float>(workspace);
+    a.counters = h->counters;
+    a.kv_len_device = ptr<const int32_t>(kv_len_device);
+    a.capacity = kv_capacity;
+    a.chunk = 64;
+    a.max_splits = (kv_capacity + 63) / 64;
+    a.qk_scale_log2 = scale * kc::kLog2e;
+    return finish(h, symbol, kc::launch_gqa_decode(Act::kF16, a, as_stream(stream)));
+}
+
+int kudacuda_qwen2_gqa_decode(void* raw, uint64_t query, uint64_t key_cache, uint64_t value_cache, uint64_t output,
+                              int64_t batch_size, int64_t query_len, int64_t kv_len, int64_t query_heads,
+                              int64_t kv_heads, int64_t head_dim, float scale, uint64_t stream) {
+    return kc::gqa_direct(raw, "qwen2_gqa_decode", Act::kF16, query, key_cache, value_cache, output,
+                          {batch_size, query_len, query_heads, kv_heads, head_dim, scale}, kv_len, stream);
+}
+
+int kudacuda_qwen2_gqa_decode_bf16(void* raw, uint64_t query, uint64_t key_cache, uint64_t value_cache,
+                                   uint64_t output, int64_t batch_size, int64_t query_len, int64_t kv_len,
+                                   int64_t query_heads, int64_t kv_heads, int64_t head_dim, float scale,
+                                   uint64_t stream) {
+    return kc::gqa_direct(raw, "qwen2_gqa_decode_bf16", Act::kBf16, query, key_cache, value_cache, output,
+                          {batch_size, query_len, query_heads, kv_heads, head_dim, scale}, kv_len, stream);
+}
+
+int kudacuda_qwen2_gqa_decode_graph(void* raw, uint64_t query, uint64_t key_cache, uint64_t value_cache,
+                                    uint64_t output, int64_t batch_size, int64_t query_len, int64_t kv_capacity,
+                                    int64_t query_heads, int64_t kv_heads, int64_t head_dim, float scale,
+                                    uint64_t kv_len_device, uint64_t stream) {
+    return kc::gqa_graph(raw, "qwen2_gqa_decode_graph", Act::kF16, query, key_cache, value_cache, output,
+                         {batch_size, query_len, query_heads, kv_heads, head_dim, scale}, kv_capacity, kv_len_device,
+                         stream);
+}
+
+int kudacuda_qwen2_gqa_decode_graph_bf16(void* raw, uint64_t query, uint64_t key_cache, uint64_t value_cache,
+                                         uint64_t output, int64_t batch_size, int64_t query_len, int64_t kv_capacity,
+                                         int64_t query_heads, int64_t kv_heads, int64_t head_dim, float scale,
+                                         uint64_t kv_len_device, uint64_t stream) {
+    return kc::gqa_graph(raw, "qwen2_gqa_decode_graph_bf16", Act::kBf16, query, key_cache, value_cache, output,
+                         {batch_size, query_len, query_heads, kv_heads, head_dim, scale}, kv_capacity, kv_len_device,
+                         stream);
+}
+
+int kudacuda_qwen2_gqa_decode_group_tiled(void* raw, uint64_t query, uint64_t key_cache, uint64_t value_cache,
+                                          uint64_t output, int64_t batch_size, int64_t query_len, int64_t kv_len,
+                                          int64_t query_heads, int64_t kv_heads, int64_t head_dim, float scale,
+                                          uint64_t stream) {
+    return kc::gqa_direct(raw, "qwen2_gqa_decode_group_tiled", Act::kF16, query, key_cache, value_cache, output,
+                          {batch_size, query_len, query_heads, kv_heads, head_dim, scale}, kv_len, stream);
+}
+
+int kudacuda_qwen2_gqa_decode_vectorized(void* raw, uint64_t query, uint64_t key_cache, uint64_t value_cache,
+                                         uint64_t output, int64_t batch_size, int64_t query_len, int64_t kv_len,
+                                         int64_t query_heads, int64_t kv_heads, int64_t head_dim, float scale,
+                                         uint64_t stream) {
+    return kc::gqa_direct(raw, "qwen2_gqa_decode_vectorized", Act::kF16, query, key_cache, value_cache, output,
+                          {batch_size, query_len, query_heads, kv_heads, head_dim, scale}, kv_len, stream);
+}
+
+int64_t kudacuda_gqa_split_chunk(int64_t kv_tokens) { return kc::gqa_chunk_for(kv_tokens < 1 ? 1 : kv_tokens); }
+
+int64_t kudacuda_gqa_workspace_floats(int64_t kv_tokens) { return kc::gqa_workspace(kv_tokens < 1 ? 1 : kv_tokens); }
+
+int kudacuda_lm_head_argmax_bf16(void* raw, uint64_t input, uint64_t norm_weight, uint64_t weight, uint64_t logits,
+                                 uint64_t argmax_out, int64_t vocab, int64_t hidden, float epsilon, uint64_t stream) {
+    Handle* h = as_handle(raw);
+    const char* symbol = "lm_head_argmax_bf16";
+    if (!ready(h, "kudacuda_lm_head_argmax_bf16")) {
+        return 1;
+    }
+    if (input == 0 || weight == 0 || argmax_out == 0) {
+        h->set_error(std::string(symbol) + " requires non-null input, weight and argmax pointers");
+        return 1;
+    }
+    if (hidden != 2048 || vocab < 1 || vocab > (int64_t{1} << 30) || (norm_weight != 0 && !(epsilon > 0.0f))) {
+        h->set_error(std::string(symbol) + " requires hidden=2048, vocab>=1, and positive epsilon");
+        return 1;
+    }
+    kc::LmHeadArgs a;
+    a.x = ptr<const uint16_t>(input);
+    a.gamma = ptr<const uint16_t>(norm_weight);
+    a.eps = epsilon;
+    a.weight = ptr<const uint16_t>(weight);
+    a.vocab = vocab;
+    a.logits = ptr<uint16_t>(logits);
+    a.block_best = h->lm_best;
+    a.counter = h->counters + 2;
+    a.argmax_out = ptr<int32_t>(argmax_out);
+    return finish(h, symbol, kc::launch_lm_head_argmax(a, as_stream(stream)));
+}
+
+int64_t kudacuda_lm_head_workspace_floats(void) { return kc::lm_head_workspace_floats(); }
+
+int kudacuda_begin_capture(void* raw, uint64_t stream) {
+    Handle* h = as_handle(raw);
+    if (h == nullptr || !h->frozen) {
+        if (h != nullptr) {
+            h->set_error("kudacuda_begin_capture requires a frozen handle");
+        }
+        return 1;
+    }
+    if (h->capturing) {
+        h->set_error("HIP graph capture is already active");
+        return 1;
+    }
+    const hipError_t status = hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeGlobal);
+    if (status != hipSuccess) {
+        h->set_hip_error("hipStreamBeginCapture", status);
+        return 1;
+    }
+    h->capturing = true;
+    h->last_error.clear();
+    return 0;
+}
+
+int kudacuda_end_capture(void* raw, uint64_t stream) {
+    Handle* h = as_handle(raw);
+    if (h == nullptr || !h->capturing) {
+        if (h != nullptr) {
+            h->set_error("kudacuda_end_capture called without active capture");
+        }
+        return 1;
+    }
+    hipGraph_t graph = nullptr;
+    const hipError_t end_status = hipStreamEndCapture(as_stream(stream), &graph);
+    h->capturing = false;
+    if (end_status != hipSuccess) {
+        h->set_hip_error("hipStreamEndCapture", end_status);
+        return 1;
+    }
+    if (h->graph_exec != nullptr) {
+        (void)hipGraphExecDestroy(h->graph_exec);
+        h->graph_exec = nullptr;
+    }
+    const hipError_t inst = hipGraphInstantiate(&h->graph_exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (inst != hipSuccess) {
+        h->graph_exec = nullptr;
+        h->set_hip_error("hipGraphInstantiate", inst);
+        return 1;
+    }
+    h->last_error.clear();
+    return 0;
+}
+
+int kudacuda_replay_graph(void* raw, uint64_t stream) {
+    Handle* h = as_handle(raw);
+    if (h == nullptr || h->graph_exec == nullptr) {
+        if (h != nullptr) {
+            h->set_error("kudacuda_replay_graph called before graph instantiation");
+        }
+        return 1;
+    }
+    return finish(h, "hipGraphLaunch", hipGraphLaunch(h->graph_exec, as_stream(stream)));
+}
+
+int kudacuda_reset_graph(void* raw) {
+    Handle* h = as_handle(raw);
+    if (h == nullptr) {
+        return 1;
+    }
+    if (h->capturing) {
+        h->set_error("kudacuda_reset_graph called during active capture");
+        return 1;
+    }
+    if (h->graph_exec != nullptr) {
+        const hipError_t status = hipGraphExecDestroy(h->graph_exec);
+        if (status != hipSuccess) {
+            h->set_hip_error("hipGraphExecDestroy", status);
+            return 1;
+        }
+        h->graph_exec = nullptr;
+    }
+    if (h->graph != nullptr) {
+        const hipError_t status = hipGraphDestroy(h->graph);
+        if (status != hipSuccess) {
+            h->set_hip_error("hipGraphDestroy", status);
+            return 1;
+        }
+        h->graph = nullptr;
+    }
+    h->last_error.clear();
+    return 0;
+}
+
+const char* kudacuda_last_error(void* raw) {
+    const Handle* h = as_handle(raw);
+    if (h == nullptr) {
+        return "invalid KudaCuda handle";
+    }
+    return h->last_error.c_str();
+}
+
+void kudacuda_destroy(void* raw) { delete as_handle(raw); }
+
+void* kudacuda_qwen2_model_create(void* raw, int64_t num_layers, int64_t vocab, int64_t kv_capacity,
+                                  float rms_epsilon, const uint64_t* layer_ptrs, const uint64_t* model_ptrs) {
+    Handle* h = as_handle(raw);
+    if (!ready(h, "kudacuda_qwen2_model_create")) {
+        return nullptr;
+    }
+    if (layer_ptrs == nullptr || model_ptrs == nullptr) {
+        h->set_error("qwen2_model_create requires layer and model pointer tables");
+        return nullptr;
+    }
+    if (num_layers < 1 || vocab < 1 || vocab > (int64_t{1} << 30) || kv_capacity < 1 ||
+        kv_capacity > kc::kMaxModelKv || !(rms_epsilon > 0.0f)) {
+        h->set_error("qwen2_model_create requires num_layers>=1, vocab>=1, kv_capacity=1..32768, positive epsilon");
+        return nullptr;
+    }
+    for (int64_t i = 0; i < num_layers * KUDACUDA_QWEN2_LAYER_FIELDS; ++i) {
+        if (layer_ptrs[i] == 0) {
+            h->set_error("qwen2_model_create: layer " + std::to_string(i / KUDACUDA_QWEN2_LAYER_FIELDS) + " field " +
+                         std::to_string(i % KUDACUDA_QWEN2_LAYER_FIELDS) + " is null");
+            return nullptr;
+        }
+    }
+    for (int i = 0; i < KUDACUDA_QWEN2_MODEL_FIELDS; ++i) {
+        if (model_ptrs[i] == 0 && i != KUDACUDA_QWEN2_LOGITS) {
+            h->set_error("qwen2_model_create: model field " + std::to_string(i) + " is null");
+            return nullptr;
+        }
+    }
+    auto* m = new (std::nothrow) kc::Model();
+    if (m == nullptr) {
+        h->set_error("qwen2_model_create: out of host memory");
+        return nullptr;
+    }
+    m->handle = h;
+    m->num_layers = num_layers;
+    m->vocab = vocab;
+    m->capacity = kv_capacity;
+    m->eps = rms_epsilon;
+    m->layers.resize(static_cast<size_t>(num_layers));
+    for (int64_t l = 0; l < num_layers; ++l) {
+        for (int f = 0; f < KUDACUDA_QWEN2_LAYER_FIELDS; ++f) {
+            m->layers[static_cast<size_t>(l)][static_cast<size_t>(f)] =
+                layer_ptrs[l * KUDACUDA_QWEN2_LAYER_FIELDS + f];
+        }
+    }
+    for (int f = 0; f < KUDACUDA_QWEN2_MODEL_FIELDS; ++f) {
+        m->g[static_cast<size_t>(f)] = model_ptrs[f];
+    }
+    h->last_error.clear();
+    return m;
+}
+
+int kudacuda_qwen2_model_step(void* raw_model, uint64_t stream) {
+    auto* m = reinterpret_cast<kc::Model*>(raw_model);
+    if (m == nullptr) {
+        return 1;
+    }
+    return finish(m->handle, "qwen2_model_step", kc::model_step(*m, as_stream(stream)));
+}
+
+int kudacuda_qwen2_model_capture(void* raw_model, uint64_t stream) {
+    auto* m = reinterpret_cast<kc::Model*>(raw_model);
+    if (m == nullptr) {
+        return 1;
+    }
+    Handle* h = m->handle;
+    if (m->exec != nullptr) {
+        (void)hipGraphExecDestroy(m->exec);
+        m->exec = nullptr;
+    }
+    hipStream_t s = as_stream(stream);
+    hipError_t status = hipStreamBeginCapture(s, hipStreamCaptureModeGlobal);
+    if (status != hipSuccess) {
+        return finish(h, "hipStreamBeginCapture", status);
+    }
+    const hipError_t launch_status = kc::model_step(*m, s);
+    hipGraph_t graph = nullptr;
+    status = hipStreamEndCapture(s, &graph);
+    if (launch_status != hipSuccess) {
+        if (graph != nullptr) {
+            (void)hipGraphDestroy(graph);
+        }
+        return finish(h, "qwen2_model_capture(step)", launch_status);
+    }
+    if (status != hipSuccess) {
+        return finish(h, "hipStreamEndCapture", status);
+    }
+    status = hipGraphInstantiate(&m->exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (status != hipSuccess) {
+        m->exec = nullptr;
+    }
+    return finish(h, "hipGraphInstantiate", status);
+}
+
+int kudacuda_qwen2_model_replay(void* raw_model, int64_t steps, uint64_t stream) {
+    auto* m = reinterpret_cast<kc::Model*>(raw_model);
+    if (m == nullptr) {
+        return 1;
+    }
+    if (m->exec == nullptr) {
+        m->handle->set_error("qwen2_model_replay called before qwen2_model_capture");
+        return 1;
+    }
+    for (int64_t i = 0; i < steps; ++i) {
+        const hipError_t status = hipGraphLaunch(m->exec, as_stream(stream));
+        if (status != hipSuccess) {
+            return finish(m->handle, "hipGraphLaunch", status);
+        }
+    }
+    m->handle->last_error.clear();
+    return 0;
+}
+
+int kudacuda_qwen2_model_time_op(void* raw_model, int64_t op, int64_t iters, uint64_t stream, float* avg_ms) {
+    auto* m = reinterpret_cast<kc::Model*>(raw_model);
+    if (m == nullptr) {
+        return 1;
+    }
+    Handle* h = m->handle;
+    if (op < 0 || op > 5 || iters < 1 || avg_ms == nullptr) {
+        h->set_error("qwen2_model_time_op requires op 0..5, iters >= 1 and an output pointer");
+        return 1;
+    }
+    hipStream_t s = as_stream(stream);
+    hipEvent_t start = nullptr, stop = nullptr;
+    hipError_t status = hipEventCreate(&start);
+    if (status == hipSuccess) {
+        status = hipEventCreate(&stop);
+    }
+    if (status == hipSuccess) {
+        status = hipEventRecord(start, s);
+    }
+    for (int64_t i = 0; i < iters && status == hipSuccess; ++i) {
+        status = kc::model_op(*m, static_cast<int>(op), i % m->num_layers, false, s);
+    }
+    if (status == hipSuccess) {
+        status = hipEventRecord(stop, s);
+    }
+    if (status == hipSuccess) {
+        status = hipEventSynchronize(stop);
+    }
+    float ms = 0.0f;
+    if (status == hipSuccess) {
+        status = hipEventElapsedTime(&ms, start, stop);
+    }
+    if (start != nullptr) {
+        (void)hipEventDestroy(start);
+    }
+    if (stop != nullptr) {
+        (void)hipEventDestroy(stop);
+    }
+    if (status == hipSuccess) {
+        *avg_ms = ms / static_cast<float>(iters);
+    }
+    return finish(h, "qwen2_model_time_op", status);
+}
+
+void kudacuda_qwen2_model_destroy(void* raw_model) { delete reinterpret_cast<kc::Model*>(raw_model); }
+
+}  // extern "C"

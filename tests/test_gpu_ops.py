@@ -1,0 +1,320 @@
+"""GPU parity of every decode-path op, called through the C ABI.
+
+Each kernel's output must equal the oracle bit for bit (integer/byte results
+and the fixed-order fp32 ops alike) and lie within the benchmark's stated
+tolerance of an fp64 textbook reference: rel 1e-2 / abs 1e-3 after bf16
+rounding.  Inputs are the BASELINE configs, seeded.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from kudacuda_amd import synthetic
+from oracle import oracle as O
+from oracle import reference as R
+from tests._gpu_util import dev, empty, host, p
+
+pytestmark = pytest.mark.gpu
+
+SEED = 20260824
+ATOL, RTOL = 1.0e-3, 1.0e-2
+
+
+def _close(actual_bits: np.ndarray, expected_f64: np.ndarray, dtype: str = "bf16", atol=ATOL, rtol=RTOL) -> None:
+    actual = O.act_to_f32(actual_bits, dtype).astype(np.float64)
+    # the fp64 reference is itself rounded to the output dtype before comparing
+    expected = O.act_to_f32(O.f32_to_act(expected_f64.astype(np.float32), dtype), dtype).astype(np.float64)
+    bad = np.abs(actual - expected) > atol + rtol * np.abs(expected)
+    assert not bad.any(), f"{bad.sum()} elements outside tolerance; max abs err {np.abs(actual - expected).max()}"
+
+
+def _bf16_round(v: np.ndarray) -> np.ndarray:
+    return O.bf16_to_f32(O.f32_to_bf16(np.asarray(v, dtype=np.float32))).astype(np.float64)
+
+
+def _quantize_gpu(torch, native, stream, w32: np.ndarray):
+    n = w32.size
+    src = dev(torch, w32.reshape(-1))
+    packed = empty(torch, n // 2, "u8")
+    absmax = empty(torch, n // 64, "f32")
+    native.call("kudacuda_nf4_quantize", p(src), 0, n, 64, p(packed), p(absmax), stream.cuda_stream)
+    stream.synchronize()
+    return packed, absmax
+
+
+def test_nf4_quantize_and_dequantize_are_bit_exact(torch_gpu, native, stream):
+    torch = torch_gpu
+    _, w = synthetic.gemv_inputs(SEED)
+    packed, absmax = _quantize_gpu(torch, native, stream, w)
+    ref_packed, ref_absmax = O.nf4_quantize(w)
+    assert np.array_equal(host(packed), ref_packed)
+    assert np.array_equal(host(absmax).view(np.uint32), ref_absmax.view(np.uint32))
+
+    n = w.size
+    out32 = empty(torch, n, "f32")
+    native.call("kudacuda_nf4_dequantize", p(packed), p(absmax), n, 64, 0, p(out32), stream.cuda_stream)
+    out16 = empty(torch, n, "u16")
+    native.call("kudacuda_nf4_dequantize", p(packed), p(absmax), n, 64, 1, p(out16), stream.cuda_stream)
+    stream.synchronize()
+    deq = O.nf4_dequantize(ref_packed, ref_absmax, n)
+    assert np.array_equal(host(out32).view(np.uint32), deq.view(np.uint32))
+    assert np.array_equal(host(out16), O.f32_to_bf16(deq))
+    # and the dequantised value is the closed form codebook[code] * absmax: the
+    # fp64 product of two fp32 values is exact, so its fp32 rounding is the
+    # correctly rounded fp32 product
+    assert np.array_equal(deq, R.nf4_dequant_f64(ref_packed, ref_absmax, n).astype(np.float32))
+
+    # bf16 input path
+    wb = synthetic.f32_to_bf16_bits(w[:256])
+    src = dev(torch, wb.reshape(-1))
+    pk = empty(torch, wb.size // 2, "u8")
+    am = empty(torch, wb.size // 64, "f32")
+    native.call("kudacuda_nf4_quantize", p(src), 1, wb.size, 64, p(pk), p(am), stream.cuda_stream)
+    stream.synchronize()
+    rp, ra = O.nf4_quantize(wb)
+    assert np.array_equal(host(pk), rp) and np.array_equal(host(am), ra)
+
+
+@pytest.mark.parametrize("with_bias,with_residual", [(False, False), (True, False), (False, True)])
+def test_nf4_gemv_config1(torch_gpu, native, stream, with_bias, with_residual):
+    torch = torch_gpu
+    x, w = synthetic.gemv_inputs(SEED)
+    packed, absmax = O.nf4_quantize(w)
+    bias = synthetic.f32_to_bf16_bits(synthetic.normal(SEED, (7,), (2048,), 0.01)) if with_bias else None
+    res = synthetic.f32_to_bf16_bits(synthetic.normal(SEED, (8,), (2048,), 1.0)) if with_residual else None
+    d_x, d_w, d_a = dev(torch, x), dev(torch, packed), dev(torch, absmax)
+    d_b = dev(torch, bias) if bias is not None else None
+    d_r = dev(torch, res) if res is not None else None
+    out = empty(torch, 2048, "u16")
+    native.call("kudacuda_nf4_gemv_bf16", p(d_x), p(d_w), p(d_a), p(d_b), p(d_r), p(out), 1, 2048, 2048, 64,
+                stream.cuda_stream)
+    stream.synchronize()
+    got = host(out)
+    assert np.array_equal(got, O.nf4_gemv2048(x, packed, absmax, 2048, bias=bias, residual=res))
+    ref = R.nf4_dequant_f64(packed, absmax, w.size).reshape(2048, 2048) @ O.bf16_to_f32(x).astype(np.float64)
+    if with_bias:
+        ref = ref + O.bf16_to_f32(bias)
+    if with_residual:
+        # residual semantics: the projection is rounded to bf16 before the add
+        ref = O.bf16_to_f32(res) + _bf16_round(ref)
+    _close(got, ref)
+
+
+@pytest.mark.parametrize("symbol,dtype,with_norm", [
+    ("kudacuda_qwen2_fused_rmsnorm_qkv_nf4_bf16", "bf16", False),
+    ("kudacuda_qwen2_fused_rmsnorm_qkv_nf4", "f16", False),
+    ("kudacuda_qwen2_fused_rmsnorm_qkv_nf4_v2", "f16", True),
+    ("kudacuda_qwen2_fused_rmsnorm_qkv_nf4_v3", "f16", True),
+])
+def test_fused_rmsnorm_qkv_config2(torch_gpu, native, stream, symbol, dtype, with_norm):
+    torch = torch_gpu
+    x, gamma, w, b = synthetic.qkv_inputs(SEED)
+    if dtype == "f16":
+        x = O.f32_to_f16(O.bf16_to_f32(x))
+        gamma = O.f32_to_f16(O.bf16_to_f32(gamma))
+        b = {k: O.f32_to_f16(O.bf16_to_f32(v)) for k, v in b.items()}
+    q = {n: O.nf4_quantize(w[n]) for n in ("q", "k", "v")}
+    d = {n: (dev(torch, q[n][0]), dev(torch, q[n][1]), dev(torch, b[n])) for n in q}
+    d_x, d_g = dev(torch, x), dev(torch, gamma)
+    qo, ko, vo = empty(torch, 2048, "u16"), empty(torch, 256, "u16"), empty(torch, 256, "u16")
+    norm = empty(torch, 2048, "f32")
+    args = [p(d_x), p(d_g)]
+    for n in ("q", "k", "v"):
+        args += [p(d[n][0]), p(d[n][1]), p(d[n][2])]
+    if with_norm:
+        args.append(p(norm))
+    args += [p(qo), p(ko), p(vo), 1, 2048, 2048, 256, 64, 1.0e-6, stream.cuda_stream]
+    native.call(symbol, *args)
+    stream.synchronize()
+    eq, ek, ev, enorm = O.qkv(x, gamma, 1.0e-6, (q["q"][0], q["q"][1], b["q"]), (q["k"][0], q["k"][1], b["k"]),
+                              (q["v"][0], q["v"][1], b["v"]), dtype=dtype, want_norm=True)
+    assert np.array_equal(host(qo), eq)
+    assert np.array_equal(host(ko), ek)
+    assert np.array_equal(host(vo), ev)
+    if with_norm:
+        assert np.array_equal(host(norm).view(np.uint32), enorm.view(np.uint32))
+    xn = R.rmsnorm_f64(O.act_to_f32(x, dtype), O.act_to_f32(gamma, dtype), 1.0e-6)
+    for n, got, rows in (("q", qo, 2048), ("k", ko, 256), ("v", vo, 256)):
+        W = R.nf4_dequant_f64(q[n][0], q[n][1], rows * 2048).reshape(rows, 2048)
+        _close(host(got), W @ xn + O.act_to_f32(b[n], dtype), dtype)
+
+
+@pytest.mark.parametrize("symbol,dtype", [("kudacuda_qwen2_swiglu_nf4_bf16", "bf16"),
+                                          ("kudacuda_qwen2_swiglu_nf4", "f16")])
+def test_swiglu(torch_gpu, native, stream, symbol, dtype):
+    torch = torch_gpu
+    x, gate, up, _ = synthetic.mlp_inputs(SEED)
+    gamma = synthetic.f32_to_bf16_bits(synthetic.normal(SEED, (9,), (2048,), 0.1) + np.float32(1.0))
+    if dtype == "f16":
+        x = O.f32_to_f16(O.bf16_to_f32(x))
+        gamma = O.f32_to_f16(O.bf16_to_f32(gamma))
+    gq, uq = O.nf4_quantize(gate), O.nf4_quantize(up)
+    d_x, d_g = dev(torch, x), dev(torch, gamma)
+    d_gw, d_ga, d_uw, d_ua = (dev(torch, a) for a in (*gq, *uq))
+    out = empty(torch, 11008, "u16")
+    native.call(symbol, p(d_x), p(d_g), p(d_gw), p(d_ga), p(d_uw), p(d_ua), p(out), 1, 2048, 11008, 64, 1.0e-6,
+                stream.cuda_stream)
+    stream.synchronize()
+    got = host(out)
+    assert np.array_equal(got, O.swiglu(x, gamma, 1.0e-6, gq, uq, dtype=dtype))
+    xn = R.rmsnorm_f64(O.act_to_f32(x, dtype), O.act_to_f32(gamma, dtype), 1.0e-6)
+    G = R.nf4_dequant_f64(*gq, gate.size).reshape(11008, 2048) @ xn
+    U = R.nf4_dequant_f64(*uq, up.size).reshape(11008, 2048) @ xn
+    _close(got, R.silu_f64(G) * U, dtype)
+
+
+@pytest.mark.parametrize("with_norm,with_residual", [(False, False), (True, True)])
+def test_mlp_config3(torch_gpu, native, stream, with_norm, with_residual):
+    torch = torch_gpu
+    x, gate, up, down = synthetic.mlp_inputs(SEED)
+    gamma = synthetic.f32_to_bf16_bits(synthetic.normal(SEED, (9,), (2048,), 0.1) + np.float32(1.0))
+    res = synthetic.f32_to_bf16_bits(synthetic.normal(SEED, (10,), (2048,), 1.0))
+    gq, uq, dq = O.nf4_quantize(gate), O.nf4_quantize(up), O.nf4_quantize(down)
+    d_x, d_g, d_r = dev(torch, x), dev(torch, gamma), dev(torch, res)
+    dd = [dev(torch, a) for a in (*gq, *uq, *dq)]
+    h = empty(torch, 11008, "u16")
+    out = empty(torch, 2048, "u16")
+    native.call("kudacuda_qwen2_mlp_nf4_bf16", p(d_x), p(d_g) if with_norm else 0, *(p(t) for t in dd), p(h),
+                p(d_r) if with_residual else 0, p(out), 1, 2048, 11008, 64, 1.0e-6, stream.cuda_stream)
+    stream.synchronize()
+    eh = O.swiglu(x, gamma if with_norm else None, 1.0e-6, gq, uq)
+    assert np.array_equal(host(h), eh)
+    eo = O.down11008(eh, *dq, residual=res if with_residual else None)
+    assert np.array_equal(host(out), eo)
+    xn = R.rmsnorm_f64(O.bf16_to_f32(x), O.bf16_to_f32(gamma) if with_norm else None, 1.0e-6)
+    G = R.nf4_dequant_f64(*gq, gate.size).reshape(11008, 2048) @ xn
+    U = R.nf4_dequant_f64(*uq, up.size).reshape(11008, 2048) @ xn
+    hh = O.bf16_to_f32(O.f32_to_bf16((R.silu_f64(G) * U).astype(np.float32))).astype(np.float64)
+    y = R.nf4_dequant_f64(*dq, down.size).reshape(2048, 11008) @ hh
+    if with_residual:
+        y = O.bf16_to_f32(res) + _bf16_round(y)
+    _close(host(out), y)
+
+
+KV_LENS = [1, 7, 37, 128, 512, 585, 1024, 2048, 8192, 32768]
+
+
+@pytest.mark.parametrize("kv_len", KV_LENS)
+def test_gqa_decode_bf16_config4(torch_gpu, native, stream, kv_len):
+    torch = torch_gpu
+    q, k, v = synthetic.gqa_inputs(SEED, kv_len)
+    d_q, d_k, d_v = dev(torch, q), dev(torch, k), dev(torch, v)
+    out = empty(torch, 2048, "u16")
+    scale = synthetic.default_scale()
+    native.call("kudacuda_qwen2_gqa_decode_bf16", p(d_q), p(d_k), p(d_v), p(out), 1, 1, kv_len, 16, 2, 128, scale,
+                stream.cuda_stream)
+    stream.synchronize()
+    got = host(out)
+    assert np.array_equal(got, O.gqa(q, k, v, kv_len))
+    ref = R.gqa_f64(O.bf16_to_f32(q), O.bf16_to_f32(k).reshape(2, kv_len, 128),
+                    O.bf16_to_f32(v).reshape(2, kv_len, 128), kv_len, scale)
+    _close(got, ref)
+    if kv_len == 1:  # a single key: the output is exactly that V row
+        assert np.array_equal(got.reshape(16, 128), np.repeat(v.reshape(2, 128), 8, axis=0))
+
+
+@pytest.mark.parametrize("kv_len,capacity", [(1, 512), (100, 512), (512, 512), (585, 2048), (2048, 2048)])
+def test_gqa_graph_reads_device_kv_len(torch_gpu, native, stream, kv_len, capacity):
+    torch = torch_gpu
+    q, k, v = synthetic.gqa_inputs(SEED, kv_len, capacity)
+    d_q, d_k, d_v = dev(torch, q), dev(torch, k), dev(torch, v)
+    d_len = dev(torch, np.array([kv_len], dtype=np.int32))
+    out = empty(torch, 2048, "u16")
+    scale = synthetic.default_scale()
+    native.call("kudacuda_qwen2_gqa_decode_graph_bf16", p(d_q), p(d_k), p(d_v), p(out), 1, 1, capacity, 16, 2, 128,
+                scale, p(d_len), stream.cuda_stream)
+    stream.synchronize()
+    assert np.array_equal(host(out), O.gqa(q, k, v, kv_len, chunk=O.gqa_chunk_for(capacity)))
+
+
+@pytest.mark.parametrize("symbol", ["kudacuda_qwen2_gqa_decode", "kudacuda_qwen2_gqa_decode_group_tiled",
+                                    "kudacuda_qwen2_gqa_decode_vectorized"])
+def test_gqa_fp16_reference_entry_points(torch_gpu, native, stream, symbol):
+    torch = torch_gpu
+    kv_len = 37
+    # reference smoke-test fixture (tests/qwen2_gqa_smoke.cu:34-63)
+    i_q = np.arange(16 * 128, dtype=np.float32)
+    i_c = np.arange(2 * kv_len * 128, dtype=np.float32)
+    q = O.f32_to_f16(np.sin(i_q * np.float32(0.017)) * np.float32(0.75))
+    k = O.f32_to_f16(np.cos(i_c * np.float32(0.011)) * np.float32(0.55)).reshape(2, kv_len, 128)
+    v = O.f32_to_f16(np.sin(i_c * np.float32(0.023)) * np.float32(0.65)).reshape(2, kv_len, 128)
+    d_q, d_k, d_v = dev(torch, q), dev(torch, k), dev(torch, v)
+    out = empty(torch, 2048, "u16")
+    scale = 1.0 / 11.313708498984761
+    native.call(symbol, p(d_q), p(d_k), p(d_v), p(out), 1, 1, kv_len, 16, 2, 128, scale, stream.cuda_stream)
+    stream.synchronize()
+    got = host(out)
+    assert np.array_equal(got, O.gqa(q, k, v, kv_len, scale=scale, dtype="f16"))
+    ref = R.gqa_f64(O.f16_to_f32(q), O.f16_to_f32(k), O.f16_to_f32(v), kv_len, scale)
+    assert np.abs(O.f16_to_f32(got) - ref).max() <= 3.5e-3  # the smoke test's tolerance
+
+
+def test_gqa_workspace_v3(torch_gpu, native, stream):
+    torch = torch_gpu
+    capacity = 512
+    scale = synthetic.default_scale()
+    ws = empty(torch, 16 * 8 * 130, "f32")
+    for kv_len in (1, 7, 64, 128, 512):  # reference tests/qwen2_gqa_workspace_smoke.cu:29-49
+        q, k, v = synthetic.gqa_inputs(SEED + kv_len, kv_len, capacity)
+        q16 = O.f32_to_f16(O.bf16_to_f32(q))
+        k16 = O.f32_to_f16(O.bf16_to_f32(k)).reshape(2, capacity, 128)
+        v16 = O.f32_to_f16(O.bf16_to_f32(v)).reshape(2, capacity, 128)
+        d_q, d_k, d_v = dev(torch, q16), dev(torch, k16), dev(torch, v16)
+        d_len = dev(torch, np.array([kv_len], dtype=np.int32))
+        out = empty(torch, 2048, "u16")
+        native.call("kudacuda_qwen2_gqa_decode_workspace_v3", p(d_q), p(d_k), p(d_v), p(out), p(ws), p(d_len), 1, 1,
+                    capacity, 16, 2, 128, scale, stream.cuda_stream)
+        stream.synchronize()
+        assert np.array_equal(host(out), O.gqa(q16, k16, v16, kv_len, chunk=64, dtype="f16"))
+
+
+@pytest.mark.parametrize("vocab,with_norm", [(151936, True), (1000, False), (1, True)])
+def test_lm_head_argmax(torch_gpu, native, stream, vocab, with_norm):
+    torch = torch_gpu
+    x = synthetic.f32_to_bf16_bits(synthetic.normal(SEED, (11,), (2048,), 1.0))
+    gamma = synthetic.final_norm_bits(SEED)
+    emb = synthetic.embedding_bits(SEED, vocab=vocab)
+    d_x, d_g, d_e = dev(torch, x), dev(torch, gamma), dev(torch, emb)
+    logits = empty(torch, vocab, "u16")
+    arg = empty(torch, 1, "i32")
+    native.call("kudacuda_lm_head_argmax_bf16", p(d_x), p(d_g) if with_norm else 0, p(d_e), p(logits), p(arg), vocab,
+                2048, 1.0e-6, stream.cuda_stream)
+    stream.synchronize()
+    tok, elog = O.lm_head_argmax(x, gamma if with_norm else None, 1.0e-6, emb)
+    assert np.array_equal(host(logits), elog)
+    assert int(host(arg)[0]) == tok
+    lf = O.bf16_to_f32(elog)
+    assert tok == int(np.argmax(lf))  # first maximum, as torch.argmax
+
+
+def test_vector_add_and_rmsnorm_plumbing(torch_gpu, native, stream):
+    torch = torch_gpu
+    a = np.arange(1000, dtype=np.float32)
+    b = np.full(1000, 0.5, dtype=np.float32)
+    d_a, d_b = dev(torch, a), dev(torch, b)
+    out = empty(torch, 1000, "f32")
+    native.call("kudacuda_vector_add", p(d_a), p(d_b), p(out), 1000, stream.cuda_stream)
+    x = np.array([[3.0, 4.0], [0.0, 1.0]], dtype=np.float32)
+    w = np.array([1.0, 0.5], dtype=np.float32)
+    d_x, d_w = dev(torch, x), dev(torch, w)
+    y = empty(torch, 4, "f32")
+    native.call("kudacuda_rmsnorm", p(d_x), p(d_w), p(y), 2, 2, 1.0e-5, stream.cuda_stream)
+    stream.synchronize()
+    assert np.array_equal(host(out), a + b)
+    # reference KAT tests/test_contracts.py:732-742
+    got = host(y).reshape(2, 2)
+    assert abs(got[0, 0] - 0.848528) < 1e-5 and abs(got[0, 1] - 0.565685) < 1e-5 and abs(got[1, 1] - 0.7071) < 1e-4
+
+
+def test_guards_reject_off_contract_shapes(torch_gpu, native, stream):
+    lib = native.lib
+    status = lib.kudacuda_qwen2_gqa_decode_bf16(native.handle, 1, 1, 1, 1, 1, 1, 0, 16, 2, 128, 0.1,
+                                                stream.cuda_stream)
+    assert status == 1 and "kv_len" in native.error()
+    status = lib.kudacuda_qwen2_fused_rmsnorm_qkv_nf4_bf16(native.handle, *([1] * 14), 1, 4096, 2048, 256, 64, 1e-6,
+                                                           stream.cuda_stream)
+    assert status == 1 and "hidden=2048" in native.error()
+    status = lib.kudacuda_nf4_gemv_bf16(native.handle, 0, 1, 1, 0, 0, 1, 1, 2048, 2048, 64, stream.cuda_stream)
+    assert status == 1 and "non-null" in native.error()

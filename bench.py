@@ -1,0 +1,239 @@
+"""Benchmark: batch-1 greedy decode of a Qwen2.5-3B-shaped NF4 model on one MI355X.
+
+Workload: 36 layers, hidden 2048, intermediate 11008,
+16/2 heads, head_dim 128, RoPE theta 1e6, QKV bias, NF4 blocksize-64 linears,
+bf16 tied embedding / lm_head (vocab 151936), seeded random init, 64 random
+prompt ids, 128 greedy tokens, KV bucket 2048.  Each step is one hipGraph
+replay of the native decode step; a "step" produces one token.
+
+Timed region: K back-to-back replays of decode steps 63..63+K-1 (the steps
+that emit the 128 greedy tokens after the 64-token prompt), inputs resident in
+HBM, bracketed by stream synchronisation.  value = K / elapsed (tok/s).
+
+Also reported: per-kernel mean launch time from HIP events on the decode
+stream (each kernel launched back to back over all 36 layers, so weights are
+not cache resident), the roofline of the kernel that dominates the step, and
+the CPU oracle (oracle/kc_oracle.c, OpenMP) timed on a bounded sample of the
+same decode on this host.
+
+Usage: python bench.py [--gpus 1] [--steps 128] [--warmup 16]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+METRIC = "bs=1 decode tok/s Qwen2.5-3B-shape NF4; kernel HBM GB/s as % of peak"
+PEAK_HBM_GBS = 8000.0
+SEED = 20260824
+PROMPT_LEN = 64
+NEW_TOKENS = 128
+KV_BUCKET = 2048
+GOLDEN = ROOT / "tests" / "golden" / "decode_qwen25_3b_nf4.json"
+
+
+def op_bytes(cfg, vocab: int, kv_len: int) -> dict[str, int]:
+    """Algorithmic HBM bytes per launch of each kernel of the decode step:
+    NF4 codes + fp32 absmax + bf16 vectors read and written once."""
+
+    h, i = cfg.hidden, cfg.intermediate
+    kv = cfg.kv_heads * cfg.head_dim
+
+    def nf4(rows: int, cols: int) -> int:
+        return rows * cols // 2 + rows * cols // 64 * 4
+
+    return {
+        "qkv_rope": nf4(h + 2 * kv, h) + 2 * (h + 2 * kv) + 2 * h * 2 + 2 * h + 2 * 2 * kv + 2 * 64 * 4,
+        "attention": 2 * h + 2 * cfg.kv_heads * kv_len * cfg.head_dim * 2 + 2 * h,  # q, K+V, out
+        "o_proj": nf4(h, h) + 2 * h * 3,
+        "gate_up": 2 * nf4(i, h) + 2 * h * 2 + 2 * i,
+        "down": nf4(h, i) + 2 * i + 2 * h * 2,
+        "lm_head": vocab * h * 2 + 2 * h * 2 + 2 * vocab,
+    }
+
+
+def step_bytes(cfg, vocab: int, kv_len: int) -> int:
+    b = op_bytes(cfg, vocab, kv_len)
+    per_layer = b["qkv_rope"] + b["attention"] + b["o_proj"] + b["gate_up"] + b["down"]
+    return cfg.layers * per_layer + b["lm_head"]
+
+
+def cpu_baseline(seconds: float, threads: int) -> dict:
+    """Time the oracle's decode step (same model, same math) on host cores."""
+
+    os.environ["OMP_NUM_THREADS"] = str(threads)
+    from kudacuda_amd import synthetic
+    from tests._host_model import HostModel
+
+    t0 = time.time()
+    model = HostModel(SEED, num_layers=36, vocab=151936, kv_capacity=KV_BUCKET, token_capacity=KV_BUCKET,
+                      threads=threads)
+    build_s = time.time() - t0
+    prompt = synthetic.prompt_ids(SEED, 1, 151936)
+    model.reset(prompt)
+    steps = 0
+    t0 = time.perf_counter()
+    while True:
+        model.step()
+        steps += 1
+        elapsed = time.perf_counter() - t0
+        if steps >= 2 and elapsed >= seconds:
+            break
+    return {
+        "value": steps / elapsed,
+        "unit": "tok/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{steps} full decode steps (36 layers + lm_head/argmax, positions 0..{steps - 1}) of the same "
+                  f"seeded model by oracle/kc_oracle.c with OpenMP, {elapsed:.1f}s timed, model build {build_s:.0f}s "
+                  "excluded",
+    }
+
+
+def main(argv: list[str] | None = None) -> int:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=NEW_TOKENS)
+    parser.add_argument("--warmup", type=int, default=16)
+    parser.add_argument("--seed", type=int, default=SEED)
+    parser.add_argument("--layers", type=int, default=36, help="debug only: any other value is not the benchmark")
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--cpu-seconds", type=float, default=12.0)
+    parser.add_argument("--op-iters", type=int, default=72)
+    args = parser.parse_args(argv)
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py runs on one GPU only: this build's decode path is a single-GPU kernel set "
+              "(no collectives); run with --gpus 1", file=sys.stderr)
+        return 2
+    if args.steps < 1 or PROMPT_LEN + args.steps > KV_BUCKET or PROMPT_LEN + args.warmup > KV_BUCKET:
+        print("steps/warmup do not fit the 2048-token KV bucket", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from kudacuda_amd import synthetic
+    from kudacuda_amd._native import Native
+    from kudacuda_amd.qwen2_decoder import Qwen2Nf4Decoder
+
+    cfg = synthetic.QWEN25_3B
+    threads = max(1, min(os.cpu_count() or 1, 16))
+    native = Native(0)
+    t0 = time.time()
+    model = Qwen2Nf4Decoder.synthetic(native, torch, seed=args.seed, num_layers=args.layers, kv_capacity=KV_BUCKET,
+                                      token_capacity=KV_BUCKET, threads=threads)
+    print(f"[bench] model built in {time.time() - t0:.1f}s ({args.layers} layers)", file=sys.stderr, flush=True)
+    stream = model.stream
+    prompt = synthetic.prompt_ids(args.seed, PROMPT_LEN, cfg.vocab)
+
+    # prompt: steps 0..62 (lm_head skipped on device until the last prompt token)
+    model.reset(prompt)
+    model.capture()
+    model.replay(PROMPT_LEN - 1)
+    # warm-up decode steps, then rewind to the first generating step
+    model.replay(args.warmup)
+    stream.synchronize()
+    model.set_step(PROMPT_LEN - 1)
+
+    torch.cuda.synchronize()
+    start_ev = torch.cuda.Event(enable_timing=True)
+    stop_ev = torch.cuda.Event(enable_timing=True)
+    start_ev.record(stream)
+    t_start = time.perf_counter()
+    model.replay(args.steps)
+    stop_ev.record(stream)
+    stream.synchronize()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t_start
+    event_ms = start_ev.elapsed_time(stop_ev)
+    tokens = model.tokens[PROMPT_LEN: PROMPT_LEN + args.steps].cpu().numpy()
+    print(f"[bench] {args.steps} steps in {elapsed * 1e3:.2f} ms (events {event_ms:.2f} ms)", file=sys.stderr,
+          flush=True)
+
+    parity = None
+    if GOLDEN.exists() and args.seed == SEED and args.layers == 36:
+        golden = json.loads(GOLDEN.read_text())
+        n = min(len(golden["tokens"]), args.steps)
+        parity = bool(np.array_equal(tokens[:n], np.asarray(golden["tokens"][:n])))
+
+    # per-kernel timing (HIP events on the decode stream, layers cycled)
+    kv_len = PROMPT_LEN + args.steps // 2
+    model.set_step(kv_len - 1)
+    per_op = {}
+    for op in ("qkv_rope", "attention", "o_proj", "gate_up", "down", "lm_head"):
+        iters = args.op_iters if op != "lm_head" else max(4, args.op_iters // 8)
+        model.time_op(op, max(2, iters // 8))  # warm
+        per_op[op] = model.time_op(op, iters)
+    launches = {"qkv_rope": args.layers, "attention": args.layers, "o_proj": args.layers, "gate_up": args.layers,
+                "down": args.layers, "lm_head": 1}
+    totals = {op: per_op[op] * launches[op] for op in per_op}
+    dominant = max(totals, key=totals.get)
+    nbytes = op_bytes(cfg, cfg.vocab, kv_len)
+    achieved = nbytes[dominant] / (per_op[dominant] * 1e-3) / 1e9
+    op_report = {
+        op: {"ms": round(per_op[op], 5), "bytes": nbytes[op],
+             "gbs": round(nbytes[op] / (per_op[op] * 1e-3) / 1e9, 1), "launches_per_step": launches[op]}
+        for op in per_op
+    }
+
+    ms_per_step = elapsed * 1e3 / args.steps
+    value = args.steps / elapsed
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "qwen2.5-3b-shape NF4 batch-1 greedy decode, hipGraph per token",
+            "layers": args.layers, "hidden": cfg.hidden, "intermediate": cfg.intermediate, "heads": "16/2x128",
+            "vocab": cfg.vocab, "weights": "nf4 blocksize 64, fp32 absmax", "activations": "bf16",
+            "prompt_len": PROMPT_LEN, "new_tokens": args.steps, "kv_bucket": KV_BUCKET, "seed": args.seed,
+        },
+        "roofline": {
+            "kernel": dominant,
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": None,
+        },
+        "step_hbm_gbs": round(step_bytes(cfg, cfg.vocab, kv_len) * value / 1e9, 1),
+        "per_kernel": op_report,
+        "token_parity_vs_oracle": parity,
+        "reference_rtx3050_fp16_tok_s": 51.825,
+    }
+    if not args.no_cpu_baseline:
+        print("[bench] timing CPU oracle baseline", file=sys.stderr, flush=True)
+        model.close()
+        del model
+        torch.cuda.empty_cache()
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds, threads)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -112,23 +112,31 @@ __device__ __forceinline__ float silu_fixed(float g) {
 }
 
 // ---------------------------------------------------------------- reductions
-__device__ __forceinline__ float wave_sum(float v) {
-    v += __shfl_xor(v, 32, 64);
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 8, 64);
-    v += __shfl_xor(v, 4, 64);
-    v += __shfl_xor(v, 2, 64);
-    v += __shfl_xor(v, 1, 64);
+// DPP row rotation (row_ror:N, rotate within each row of 16 lanes).
+template <int N>
+__device__ __forceinline__ float row_ror(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 | N, 0xf, 0xf, false));
+}
+
+// Butterfly over the 16 lanes of a row: v += partner for partner distance
+// 8, 4, 2, 1.  Implemented with row rotations: after the distance-8 stage the
+// row holds a period-8 pattern, after distance 4 a period-4 one, ..., so a
+// rotation by d pairs every lane with the same value as lane ^ d, and the sums
+// equal the xor butterfly's bit for bit (IEEE addition is commutative).
+__device__ __forceinline__ float group16_sum(float v) {
+    v += row_ror<8>(v);
+    v += row_ror<4>(v);
+    v += row_ror<2>(v);
+    v += row_ror<1>(v);
     return v;
 }
 
-// Butterfly over the 16 lanes of a row (o = 8,4,2,1).
-__device__ __forceinline__ float group16_sum(float v) {
-    v += __shfl_xor(v, 8, 64);
-    v += __shfl_xor(v, 4, 64);
-    v += __shfl_xor(v, 2, 64);
-    v += __shfl_xor(v, 1, 64);
-    return v;
+// Butterfly over the wave: partner distance 32, 16 (cross-row shuffles), then
+// the in-row stages 8..1.  Every lane ends with the same value.
+__device__ __forceinline__ float wave_sum(float v) {
+    v += __shfl_xor(v, 32, 64);
+    v += __shfl_xor(v, 16, 64);
+    return group16_sum(v);
 }
 
 // ------------------------------------------------------------------ NF4 dots

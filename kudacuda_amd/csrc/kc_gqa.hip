@@ -1,18 +1,33 @@
 // Split-KV grouped-query decode attention for the Qwen2.5-3B shape
-// (16 query heads, 2 KV heads, group 8, head_dim 128), one launch per call.
+// (16 query heads, 2 KV heads, group 8, head_dim 128).
 //
-// Grid (max_splits, 2): block (s, g) owns tokens [s*C, min(s*C+C, L)) of KV
-// head g and serves all 8 query heads of the group, so every K/V byte is read
-// once.  A block is 4 waves = 16 groups of 16 lanes; lane li of a group holds
-// dims [8li, 8li+8) of all 8 query heads.  Per 64-token round, group gi takes
-// tokens base + 4gi + {0..3}: 8 dot products of 8 dims per lane, a 16-lane
-// butterfly, then an online-softmax update in the log2 domain (scores are
-// pre-multiplied by scale*log2e and exponentiated with exp2_fixed).
-// The 16 group states are merged through LDS, each block writes one
-// (max, sum, acc[128]) partial per head, and the last block of a KV head to
-// finish (device-scope ticket) merges the splits and writes the output.  The
-// ticket counter is reset by that block, so the launch is capture-safe and
-// needs no memset.  kv_len may come from device memory (graph replay).
+// Partial kernel, grid (max_splits, 2): block (s, g) owns tokens
+// [s*C, min(s*C+C, L)) of KV head g and serves all 8 query heads of the
+// group, so every K/V byte is read once.  A block is 8 waves = 32 groups of 16
+// lanes; lane li of a group holds dims [8li, 8li+8) of all 8 query heads.  Per
+// 128-token round, group gi takes tokens base + 4gi + {0..3}: 8 dot products
+// of 8 dims per lane and a 16-lane butterfly (DPP) give every lane of the group
+// all 32 (token, head) scores (log2 domain: pre-multiplied by scale*log2e).
+// The running max is updated redundantly (cheap), but each exponential is
+// computed once: lane li evaluates exp2_fixed for (token, head) slots li and
+// li+16 and the rescale factor of head li, exchanged through a per-group LDS
+// slot (all lanes of a group are in one wave, so no barrier is needed).  The
+// next round's K/V rows are loaded before the current round is reduced, and
+// split 0 issues its first rows before kv_len arrives.
+// The 32 group states are merged through LDS (weights exp2(m_g - M) computed
+// once per group and head) into one (max, sum, acc[128]) split partial per
+// head.  Then:
+//   * a single split finishes in place: out = acc*1 / (sum*1), the general
+//     merge formula with weight exp2(0) = 1 (no ticket, no fences);
+//   * up to kInKernelSplits splits: the partial is written and the last block
+//     of the KV head to finish (device-scope ticket, reset by that block, so
+//     the launch is capture-safe) merges the splits;
+//   * more splits: the partials are merged by gqa_merge_kernel (grid: query
+//     head x 16-dim slice; partials staged through LDS in one pass) launched
+//     right after.
+// Every path sums the splits in index order with the same operations, so the
+// result depends only on (inputs, kv_len, C).  kv_len may come from device
+// memory (graph replay); C comes from the cache length (gqa_chunk_for).
 //
 // Math follows the reference's split-KV workspace kernels
 // (kernels/common/qwen2_gqa_workspace.cuh:13-120: per-tile max, sum and
@@ -25,33 +40,79 @@
 namespace kc {
 namespace {
 
-constexpr int kGqaThreads = 256;
-constexpr int kGroups = 16;
+constexpr int kGqaWaves = 8;
+constexpr int kGqaThreads = 64 * kGqaWaves;
+constexpr int kGroups = 4 * kGqaWaves;      // 16-lane groups per block
+constexpr int kRoundTokens = 4 * kGroups;   // tokens per round
 constexpr int kHeadsPerGroup = 8;
 constexpr int kDim = 128;
 constexpr int kPartialStride = 2 + kDim;
+constexpr int kInKernelSplits = 16;
+constexpr int kMergeMaxSplits = 1024;
+constexpr int kMergeDims = 16;              // dims per merge block
+constexpr int kSlot = 40;                   // per-group LDS exchange: 32 scores + 8 rescales
+constexpr float kNegInf = -__builtin_huge_valf();
+
+__device__ __forceinline__ int64_t read_kv_len(const GqaArgs& a) {
+    int64_t L = a.kv_len_device != nullptr ? static_cast<int64_t>(*a.kv_len_device) + a.kv_len_offset : a.kv_len_host;
+    return L < 0 ? 0 : (L > a.capacity ? a.capacity : L);
+}
+
+__device__ __forceinline__ void load_round(const uint16_t* kbase, const uint16_t* vbase, int64_t tk, int nvalid,
+                                           uint4* kr, uint4* vr) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        if (k < nvalid) {
+            kr[k] = *reinterpret_cast<const uint4*>(kbase + (tk + k) * kDim);
+            vr[k] = *reinterpret_cast<const uint4*>(vbase + (tk + k) * kDim);
+        } else {
+            kr[k] = make_uint4(0, 0, 0, 0);
+            vr[k] = make_uint4(0, 0, 0, 0);
+        }
+    }
+}
+
+__device__ __forceinline__ int clamp4(int64_t n) { return static_cast<int>(n < 0 ? 0 : (n > 4 ? 4 : n)); }
 
 template <typename T>
-__global__ __launch_bounds__(kGqaThreads) void gqa_split_kernel(GqaArgs a) {
-    __shared__ float s_m[kGroups][kHeadsPerGroup];
-    __shared__ float s_l[kGroups][kHeadsPerGroup];
+__global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a, int merge_mode) {
+    __shared__ float s_x[kGroups][kSlot];
+    // group states, head-major so a thread reads one head's 32 groups as
+    // 8 contiguous 16-byte loads
+    __shared__ __attribute__((aligned(16))) float s_m[kHeadsPerGroup][kGroups];
+    __shared__ __attribute__((aligned(16))) float s_l[kHeadsPerGroup][kGroups];
+    __shared__ __attribute__((aligned(16))) float s_w[kHeadsPerGroup][kGroups];
+    __shared__ float s_M[kHeadsPerGroup];
+    __shared__ float s_L[kHeadsPerGroup];
     __shared__ float s_acc[kGroups][kHeadsPerGroup / 2][kDim];  // half the heads at a time
+    __shared__ float s_sw[kInKernelSplits][kHeadsPerGroup];
     __shared__ int s_last;
 
     const int g = blockIdx.y;
     const int64_t s = blockIdx.x;
-    int64_t L = a.kv_len_device != nullptr ? static_cast<int64_t>(*a.kv_len_device) + a.kv_len_offset : a.kv_len_host;
-    L = L < 0 ? 0 : (L > a.capacity ? a.capacity : L);
-    const int64_t C = a.chunk;
-    const int64_t nsplit = (L + C - 1) / C;
-    if (s >= nsplit) {
-        return;
-    }
-
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int gi = wave * 4 + (lane >> 4);
     const int li = lane & 15;
+    const int64_t C = a.chunk;
+    const uint16_t* kbase = a.k + static_cast<int64_t>(g) * a.capacity * kDim + 8 * li;
+    const uint16_t* vbase = a.v + static_cast<int64_t>(g) * a.capacity * kDim + 8 * li;
+    const int64_t t0 = s * C;
+
+    // Split 0 always exists once kv_len >= 1: its first rows (bounded by the
+    // capacity) are requested before kv_len is known.
+    uint4 kr[4], vr[4];
+    int spec = 0;
+    if (s == 0) {
+        spec = clamp4(a.capacity - 4 * gi);
+        load_round(kbase, vbase, 4 * gi, spec, kr, vr);
+    }
+    const int64_t L = read_kv_len(a);
+    const int64_t nsplit = (L + C - 1) / C;
+    if (s >= nsplit) {
+        return;
+    }
+    const int64_t tend = (t0 + C < L) ? t0 + C : L;
 
     float q[kHeadsPerGroup][8];
 #pragma unroll
@@ -59,41 +120,39 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_split_kernel(GqaArgs a) {
         const uint4 v = *reinterpret_cast<const uint4*>(a.q + (g * kHeadsPerGroup + hl) * kDim + 8 * li);
         unpack8<T>(v, q[hl]);
     }
-    float m[kHeadsPerGroup], l[kHeadsPerGroup], acc[kHeadsPerGroup][8];
+    // softmax state of head li lives in lane li (< 8) of each group
+    float m_own = kNegInf, l_own = 0.0f;
+    float acc[kHeadsPerGroup][8];
 #pragma unroll
     for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
-        m[hl] = -__builtin_huge_valf();
-        l[hl] = 0.0f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             acc[hl][j] = 0.0f;
         }
     }
+    float* slot = s_x[gi];
 
-    const uint16_t* kbase = a.k + static_cast<int64_t>(g) * a.capacity * kDim + 8 * li;
-    const uint16_t* vbase = a.v + static_cast<int64_t>(g) * a.capacity * kDim + 8 * li;
-    const int64_t t0 = s * C;
-    const int64_t tend = (t0 + C < L) ? t0 + C : L;
-    for (int64_t base = t0; base < tend; base += 64) {
-        const int64_t tk = base + 4 * gi;
-        int nvalid = static_cast<int>(tend - tk);
-        nvalid = nvalid < 0 ? 0 : (nvalid > 4 ? 4 : nvalid);
-        uint4 kr[4], vr[4];
+    if (s != 0) {
+        load_round(kbase, vbase, t0 + 4 * gi, clamp4(tend - (t0 + 4 * gi)), kr, vr);
+    }
+    for (int64_t base = t0; base < tend; base += kRoundTokens) {
+        const int cur_valid = clamp4(tend - (base + 4 * gi));
+        uint4 ck[4], cv[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            if (k < nvalid) {
-                kr[k] = *reinterpret_cast<const uint4*>(kbase + (tk + k) * kDim);
-                vr[k] = *reinterpret_cast<const uint4*>(vbase + (tk + k) * kDim);
-            } else {
-                kr[k] = make_uint4(0, 0, 0, 0);
-                vr[k] = make_uint4(0, 0, 0, 0);
-            }
+            ck[k] = kr[k];
+            cv[k] = vr[k];
         }
-        float s2[4][kHeadsPerGroup];
+        const int64_t nbase = base + kRoundTokens;
+        if (nbase < tend) {  // next round's rows load while this one computes
+            load_round(kbase, vbase, nbase + 4 * gi, clamp4(tend - (nbase + 4 * gi)), kr, vr);
+        }
+
+        // scores: every lane of the group gets the sums, lane 0 files them
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             float kf[8];
-            unpack8<T>(kr[k], kf);
+            unpack8<T>(ck[k], kf);
 #pragma unroll
             for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
                 float d = 0.0f;
@@ -101,57 +160,116 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_split_kernel(GqaArgs a) {
                 for (int j = 0; j < 8; ++j) {
                     d = fmaf(q[hl][j], kf[j], d);
                 }
-                s2[k][hl] = group16_sum(d) * a.qk_scale_log2;
-            }
-        }
-        if (nvalid == 0) {
-            continue;
-        }
-        float vf[4][8];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            unpack8<T>(vr[k], vf[k]);
-        }
-#pragma unroll
-        for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
-            float mt = -__builtin_huge_valf();
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                if (k < nvalid) {
-                    mt = fmaxf(mt, s2[k][hl]);
+                const float sc = group16_sum(d) * a.qk_scale_log2;
+                if (li == 0) {
+                    slot[k * 8 + hl] = sc;
                 }
             }
-            const float mnew = fmaxf(m[hl], mt);
-            const float corr = exp2_fixed(m[hl] - mnew);
-            l[hl] = l[hl] * corr;
+        }
+        if (cur_valid == 0) {
+            continue;
+        }
+        __builtin_amdgcn_wave_barrier();
+        // lane li < 8: online-softmax step of head li; slot k*8+li becomes
+        // p = exp2(s - m_new), slot 32+li the rescale exp2(m_old - m_new)
+        if (li < kHeadsPerGroup) {
+            float sc[4];
+            float mt = kNegInf;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                sc[k] = slot[k * 8 + li];
+                if (k < cur_valid) {
+                    mt = fmaxf(mt, sc[k]);
+                }
+            }
+            const float mnew = fmaxf(m_own, mt);
+            const float corr = exp2_fixed(m_own - mnew);
+            l_own = l_own * corr;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if (k < cur_valid) {
+                    const float p = exp2_fixed(sc[k] - mnew);
+                    l_own = l_own + p;
+                    slot[k * 8 + li] = p;
+                }
+            }
+            slot[32 + li] = corr;
+            m_own = mnew;
+        }
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
+            const float corr = slot[32 + hl];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 acc[hl][j] = acc[hl][j] * corr;
             }
+        }
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                if (k < nvalid) {
-                    const float p = exp2_fixed(s2[k][hl] - mnew);
-                    l[hl] = l[hl] + p;
+        for (int k = 0; k < 4; ++k) {
+            if (k < cur_valid) {
+                float vf[8];
+                unpack8<T>(cv[k], vf);
+#pragma unroll
+                for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
+                    const float p = slot[k * 8 + hl];
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
-                        acc[hl][j] = fmaf(p, vf[k][j], acc[hl][j]);
+                        acc[hl][j] = fmaf(p, vf[j], acc[hl][j]);
                     }
                 }
             }
-            m[hl] = mnew;
         }
+        __builtin_amdgcn_wave_barrier();
     }
 
-    // ---- merge the 16 group states of this block (per head, groups in order)
-    if (li == 0) {
+    // ---- merge the group states of this block (per head, groups in order;
+    // a group that saw no token is skipped)
+    if (li < kHeadsPerGroup) {
+        s_m[li][gi] = m_own;
+        s_l[li][gi] = l_own;
+    }
+    __syncthreads();
+    if (threadIdx.x < kGroups * kHeadsPerGroup) {
+        const int hl = threadIdx.x / kGroups;
+        const int gg = threadIdx.x % kGroups;
+        float mv[kGroups];
 #pragma unroll
-        for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
-            s_m[gi][hl] = m[hl];
-            s_l[gi][hl] = l[hl];
+        for (int x = 0; x < kGroups; ++x) {
+            mv[x] = s_m[hl][x];
+        }
+        float M = kNegInf;
+#pragma unroll
+        for (int x = 0; x < kGroups; ++x) {
+            M = fmaxf(M, mv[x]);
+        }
+        const float mg = s_m[hl][gg];
+        s_w[hl][gg] = mg == kNegInf ? 0.0f : exp2_fixed(mg - M);
+        if (gg == 0) {
+            s_M[hl] = M;
         }
     }
-    float* part = a.partials;
+    __syncthreads();
+    if (threadIdx.x < kHeadsPerGroup) {
+        const int hl = threadIdx.x;
+        float mv[kGroups], lv[kGroups], wv[kGroups];
+#pragma unroll
+        for (int x = 0; x < kGroups; ++x) {
+            mv[x] = s_m[hl][x];
+            lv[x] = s_l[hl][x];
+            wv[x] = s_w[hl][x];
+        }
+        float lsum = 0.0f;
+#pragma unroll
+        for (int x = 0; x < kGroups; ++x) {
+            const float t = fmaf(lv[x], wv[x], lsum);
+            lsum = mv[x] != kNegInf ? t : lsum;
+        }
+        s_L[hl] = lsum;
+    }
+
+    // merged acc of the block: thread t owns (hl = half*4 + t/128, d = t%128)
+    float av_out[2];
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
         __syncthreads();
@@ -163,32 +281,53 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_split_kernel(GqaArgs a) {
             }
         }
         __syncthreads();
-        for (int idx = threadIdx.x; idx < (kHeadsPerGroup / 2) * kDim; idx += kGqaThreads) {
-            const int hh = idx / kDim;
-            const int d = idx % kDim;
-            const int hl = half * 4 + hh;
-            float M = -__builtin_huge_valf();
-            for (int gg = 0; gg < kGroups; ++gg) {
-                M = fmaxf(M, s_m[gg][hl]);
-            }
-            float lsum = 0.0f, av = 0.0f;
-            for (int gg = 0; gg < kGroups; ++gg) {
-                const float mg = s_m[gg][hl];
-                if (mg == -__builtin_huge_valf()) {
-                    continue;
-                }
-                const float w = exp2_fixed(mg - M);
-                lsum = fmaf(s_l[gg][hl], w, lsum);
-                av = fmaf(s_acc[gg][hh][d], w, av);
-            }
-            const int64_t h = g * kHeadsPerGroup + hl;
-            float* dst = part + (h * a.max_splits + s) * kPartialStride;
-            dst[2 + d] = av;
-            if (d == 0) {
-                dst[0] = M;
-                dst[1] = lsum;
-            }
+        const int hh = threadIdx.x / kDim;
+        const int d = threadIdx.x % kDim;
+        const int hl = half * 4 + hh;
+        float mv[kGroups], wv[kGroups], xv[kGroups];
+#pragma unroll
+        for (int x = 0; x < kGroups; ++x) {
+            mv[x] = s_m[hl][x];
+            wv[x] = s_w[hl][x];
+            xv[x] = s_acc[x][hh][d];
         }
+        float av = 0.0f;
+#pragma unroll
+        for (int x = 0; x < kGroups; ++x) {
+            const float t = fmaf(xv[x], wv[x], av);
+            av = mv[x] != kNegInf ? t : av;
+        }
+        av_out[half] = av;
+    }
+
+    if (nsplit == 1 && merge_mode != 2) {
+        // single split: the general merge with weight exp2(M - M) = 1
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const int hl = half * 4 + threadIdx.x / kDim;
+            const int d = threadIdx.x % kDim;
+            const float w = exp2_fixed(s_M[hl] - s_M[hl]);
+            const float lt = fmaf(s_L[hl], w, 0.0f);
+            const float o = fmaf(av_out[half], w, 0.0f);
+            a.out[(g * kHeadsPerGroup + hl) * kDim + d] = T::store(o / lt);
+        }
+        return;
+    }
+
+    float* part = a.partials;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        const int hl = half * 4 + threadIdx.x / kDim;
+        const int d = threadIdx.x % kDim;
+        float* dst = part + ((g * kHeadsPerGroup + hl) * a.max_splits + s) * kPartialStride;
+        dst[2 + d] = av_out[half];
+        if (d == 0) {
+            dst[0] = s_M[hl];
+            dst[1] = s_L[hl];
+        }
+    }
+    if (merge_mode == 2) {
+        return;  // gqa_merge_kernel follows
     }
 
     // ---- ticket: the last block of this KV head merges all splits
@@ -206,45 +345,154 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_split_kernel(GqaArgs a) {
     if (threadIdx.x == 0) {
         a.counters[g] = 0u;
     }
-    for (int idx = threadIdx.x; idx < kHeadsPerGroup * kDim; idx += kGqaThreads) {
+    if (threadIdx.x < kHeadsPerGroup * kInKernelSplits) {
+        const int hl = threadIdx.x / kInKernelSplits;
+        const int ss = threadIdx.x % kInKernelSplits;
+        const float* src = part + (g * kHeadsPerGroup + hl) * a.max_splits * kPartialStride;
+        float mv[kInKernelSplits];
+#pragma unroll
+        for (int x = 0; x < kInKernelSplits; ++x) {
+            mv[x] = x < nsplit ? src[x * kPartialStride] : kNegInf;
+        }
+        float M = kNegInf;
+#pragma unroll
+        for (int x = 0; x < kInKernelSplits; ++x) {
+            M = fmaxf(M, mv[x]);
+        }
+        if (ss < nsplit) {
+            s_sw[ss][hl] = exp2_fixed(src[ss * kPartialStride] - M);
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < kHeadsPerGroup) {
+        const int hl = threadIdx.x;
+        const float* src = part + (g * kHeadsPerGroup + hl) * a.max_splits * kPartialStride;
+        float lv[kInKernelSplits];
+#pragma unroll
+        for (int x = 0; x < kInKernelSplits; ++x) {
+            lv[x] = x < nsplit ? src[x * kPartialStride + 1] : 0.0f;
+        }
+        float lt = 0.0f;
+#pragma unroll
+        for (int x = 0; x < kInKernelSplits; ++x) {
+            if (x < nsplit) {
+                lt = fmaf(lv[x], s_sw[x][hl], lt);
+            }
+        }
+        s_L[hl] = lt;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int idx = threadIdx.x + k * kGqaThreads;
         const int hl = idx / kDim;
         const int d = idx % kDim;
-        const int64_t h = g * kHeadsPerGroup + hl;
-        const float* src = part + h * a.max_splits * kPartialStride;
-        float M = -__builtin_huge_valf();
-        for (int64_t ss = 0; ss < nsplit; ++ss) {
-            M = fmaxf(M, src[ss * kPartialStride]);
+        const float* src = part + (g * kHeadsPerGroup + hl) * a.max_splits * kPartialStride + 2 + d;
+        float vals[kInKernelSplits];
+#pragma unroll
+        for (int x = 0; x < kInKernelSplits; ++x) {
+            vals[x] = x < nsplit ? src[x * kPartialStride] : 0.0f;
         }
-        float lt = 0.0f, o = 0.0f;
-        for (int64_t ss = 0; ss < nsplit; ++ss) {
-            const float* p = src + ss * kPartialStride;
-            const float w = exp2_fixed(p[0] - M);
-            lt = fmaf(p[1], w, lt);
-            o = fmaf(p[2 + d], w, o);
+        float o = 0.0f;
+#pragma unroll
+        for (int x = 0; x < kInKernelSplits; ++x) {
+            if (x < nsplit) {
+                o = fmaf(vals[x], s_sw[x][hl], o);
+            }
         }
-        a.out[h * kDim + d] = T::store(o / lt);
+        a.out[(g * kHeadsPerGroup + hl) * kDim + d] = T::store(o / s_L[hl]);
+    }
+}
+
+// grid (16 query heads, 128 / kMergeDims): M* over the splits (order-free
+// max), weights exp2(M_s - M*), then the split sums and the weighted acc
+// summed in split order from LDS-staged partials.
+template <typename T>
+__global__ __launch_bounds__(256) void gqa_merge_kernel(GqaArgs a) {
+    __shared__ float s_w[kMergeMaxSplits];
+    __shared__ float s_v[kMergeMaxSplits / 4][kMergeDims];  // one quarter of the splits at a time
+    __shared__ float s_red[256];
+    __shared__ float s_lt;
+    const int h = blockIdx.x;
+    const int d0 = blockIdx.y * kMergeDims;
+    const int64_t L = read_kv_len(a);
+    const int64_t nsplit = (L + a.chunk - 1) / a.chunk;
+    if (nsplit < 1) {
+        return;
+    }
+    const float* src = a.partials + static_cast<int64_t>(h) * a.max_splits * kPartialStride;
+    float M = kNegInf;
+    for (int64_t x = threadIdx.x; x < nsplit; x += 256) {
+        M = fmaxf(M, src[x * kPartialStride]);
+    }
+    s_red[threadIdx.x] = M;
+    __syncthreads();
+    for (int o = 128; o >= 1; o >>= 1) {
+        if (threadIdx.x < o) {
+            s_red[threadIdx.x] = fmaxf(s_red[threadIdx.x], s_red[threadIdx.x + o]);
+        }
+        __syncthreads();
+    }
+    M = s_red[0];
+    for (int64_t x = threadIdx.x; x < nsplit; x += 256) {
+        s_w[x] = exp2_fixed(src[x * kPartialStride] - M);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float lt = 0.0f;
+        for (int64_t x = 0; x < nsplit; ++x) {
+            lt = fmaf(src[x * kPartialStride + 1], s_w[x], lt);
+        }
+        s_lt = lt;
+    }
+    float o = 0.0f;
+    const int d = threadIdx.x;  // threads < kMergeDims accumulate
+    constexpr int64_t kTile = kMergeMaxSplits / 4;
+    for (int64_t x0 = 0; x0 < nsplit; x0 += kTile) {
+        const int64_t n = (nsplit - x0 < kTile) ? nsplit - x0 : kTile;
+        __syncthreads();
+        for (int64_t e = threadIdx.x; e < n * kMergeDims; e += 256) {
+            const int64_t x = e / kMergeDims;
+            const int dd = static_cast<int>(e % kMergeDims);
+            s_v[x][dd] = src[(x0 + x) * kPartialStride + 2 + d0 + dd];
+        }
+        __syncthreads();
+        if (d < kMergeDims) {
+            for (int64_t x = 0; x < n; ++x) {
+                o = fmaf(s_v[x][d], s_w[x0 + x], o);
+            }
+        }
+    }
+    __syncthreads();
+    if (d < kMergeDims) {
+        a.out[static_cast<int64_t>(h) * kDim + d0 + d] = T::store(o / s_lt);
     }
 }
 
 }  // namespace
 
-int64_t gqa_chunk_for(int64_t tokens) {
-    int64_t chunk = 64;
-    while ((tokens + chunk - 1) / chunk > 128) {
-        chunk *= 2;
-    }
-    return chunk;
-}
+int64_t gqa_chunk_for(int64_t) { return 2 * kRoundTokens; }
 
 hipError_t launch_gqa_decode(Act act, const GqaArgs& a, hipStream_t stream) {
-    if (a.max_splits <= 0) {
-        return hipSuccess;
+    if (a.max_splits <= 0 || a.max_splits > kMergeMaxSplits || a.chunk <= 0 || a.chunk % kRoundTokens != 0) {
+        return hipErrorInvalidValue;
     }
+    const int merge_mode = a.max_splits <= kInKernelSplits ? 1 : 2;
     const dim3 grid(static_cast<unsigned>(a.max_splits), 2);
     if (act == Act::kBf16) {
-        hipLaunchKernelGGL(gqa_split_kernel<Bf16>, grid, dim3(kGqaThreads), 0, stream, a);
+        hipLaunchKernelGGL(gqa_partial_kernel<Bf16>, grid, dim3(kGqaThreads), 0, stream, a, merge_mode);
     } else {
-        hipLaunchKernelGGL(gqa_split_kernel<F16>, grid, dim3(kGqaThreads), 0, stream, a);
+        hipLaunchKernelGGL(gqa_partial_kernel<F16>, grid, dim3(kGqaThreads), 0, stream, a, merge_mode);
+    }
+    hipError_t status = hipGetLastError();
+    if (status != hipSuccess || merge_mode == 1) {
+        return status;
+    }
+    const dim3 mgrid(16, kDim / kMergeDims);
+    if (act == Act::kBf16) {
+        hipLaunchKernelGGL(gqa_merge_kernel<Bf16>, mgrid, dim3(256), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL(gqa_merge_kernel<F16>, mgrid, dim3(256), 0, stream, a);
     }
     return hipGetLastError();
 }

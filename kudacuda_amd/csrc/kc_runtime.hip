@@ -824,8 +824,8 @@ int kudacuda_qwen2_gqa_decode_workspace_v3(void* raw, uint64_t query, uint64_t k
     a.counters = h->counters;
     a.kv_len_device = ptr<const int32_t>(kv_len_device);
     a.capacity = kv_capacity;
-    a.chunk = 64;
-    a.max_splits = (kv_capacity + 63) / 64;
+    a.chunk = kc::gqa_chunk_for(kv_capacity);
+    a.max_splits = (kv_capacity + a.chunk - 1) / a.chunk;
     a.qk_scale_log2 = scale * kc::kLog2e;
     return finish(h, symbol, kc::launch_gqa_decode(Act::kF16, a, as_stream(stream)));
 }

@@ -365,13 +365,15 @@ KCO_API void kco_down11008(int act, const uint16_t* x, const uint8_t* w, const f
 }
 
 /* ------------------------------------------------------------------- GQA */
-KCO_API int64_t kco_gqa_chunk_for(int64_t tokens) {
-    int64_t chunk = 64;
-    while ((tokens + chunk - 1) / chunk > 128) chunk *= 2;
-    return chunk;
-}
+/* Block shape of the kernel: GQA_GROUPS groups of 16 lanes; a round covers
+ * GQA_ROUND = 4 * GQA_GROUPS tokens (group gi takes base + 4gi + {0..3}). */
+#define GQA_GROUPS 32
+#define GQA_ROUND (4 * GQA_GROUPS)
 
-/* q [16,128], caches [2, capacity, 128], kv_len L, chunk C. */
+/* tokens per split for a cache of `tokens` rows (the kernels' rule) */
+KCO_API int64_t kco_gqa_chunk_for(int64_t tokens) { (void)tokens; return 2 * GQA_ROUND; }
+
+/* q [16,128], caches [2, capacity, 128], kv_len L, chunk C (multiple of GQA_ROUND). */
 KCO_API void kco_gqa(int act, const uint16_t* q, const uint16_t* kc, const uint16_t* vc, int64_t capacity,
                      int64_t L, int64_t C, float qk_scale_log2, uint16_t* out) {
     if (L > capacity) L = capacity;
@@ -384,9 +386,9 @@ KCO_API void kco_gqa(int act, const uint16_t* q, const uint16_t* kc, const uint1
             float qf[8][128];
             for (int hl = 0; hl < 8; ++hl)
                 for (int d = 0; d < 128; ++d) qf[hl][d] = act_load(act, q[(8 * g + hl) * 128 + d]);
-            float gm[16][8], gl[16][8];
-            static __thread float gacc[16][8][128];
-            for (int gi = 0; gi < 16; ++gi)
+            float gm[GQA_GROUPS][8], gl[GQA_GROUPS][8];
+            static __thread float gacc[GQA_GROUPS][8][128];
+            for (int gi = 0; gi < GQA_GROUPS; ++gi)
                 for (int hl = 0; hl < 8; ++hl) {
                     gm[gi][hl] = -INFINITY;
                     gl[gi][hl] = 0.0f;
@@ -394,8 +396,8 @@ KCO_API void kco_gqa(int act, const uint16_t* q, const uint16_t* kc, const uint1
                 }
             const int64_t t0 = s * C;
             const int64_t tend = (t0 + C < L) ? t0 + C : L;
-            for (int64_t base = t0; base < tend; base += 64) {
-                for (int gi = 0; gi < 16; ++gi) {
+            for (int64_t base = t0; base < tend; base += GQA_ROUND) {
+                for (int gi = 0; gi < GQA_GROUPS; ++gi) {
                     const int64_t tk = base + 4 * gi;
                     int nvalid = (int)(tend - tk);
                     nvalid = nvalid < 0 ? 0 : (nvalid > 4 ? 4 : nvalid);
@@ -434,16 +436,16 @@ KCO_API void kco_gqa(int act, const uint16_t* q, const uint16_t* kc, const uint1
             }
             for (int hl = 0; hl < 8; ++hl) {
                 float M = -INFINITY;
-                for (int gi = 0; gi < 16; ++gi) M = fmaxf(M, gm[gi][hl]);
+                for (int gi = 0; gi < GQA_GROUPS; ++gi) M = fmaxf(M, gm[gi][hl]);
                 float* dst = part + ((int64_t)(8 * g + hl) * nsplit + s) * 130;
                 float lsum = 0.0f;
-                for (int gi = 0; gi < 16; ++gi) {
+                for (int gi = 0; gi < GQA_GROUPS; ++gi) {
                     if (gm[gi][hl] == -INFINITY) continue;
                     lsum = fmaf(gl[gi][hl], exp2_fixed(gm[gi][hl] - M), lsum);
                 }
                 for (int d = 0; d < 128; ++d) {
                     float av = 0.0f;
-                    for (int gi = 0; gi < 16; ++gi) {
+                    for (int gi = 0; gi < GQA_GROUPS; ++gi) {
                         if (gm[gi][hl] == -INFINITY) continue;
                         av = fmaf(gacc[gi][hl][d], exp2_fixed(gm[gi][hl] - M), av);
                     }

@@ -267,7 +267,7 @@ def test_gqa_workspace_v3(torch_gpu, native, stream):
         native.call("kudacuda_qwen2_gqa_decode_workspace_v3", p(d_q), p(d_k), p(d_v), p(out), p(ws), p(d_len), 1, 1,
                     capacity, 16, 2, 128, scale, stream.cuda_stream)
         stream.synchronize()
-        assert np.array_equal(host(out), O.gqa(q16, k16, v16, kv_len, chunk=64, dtype="f16"))
+        assert np.array_equal(host(out), O.gqa(q16, k16, v16, kv_len, chunk=O.gqa_chunk_for(capacity), dtype="f16"))
 
 
 @pytest.mark.parametrize("vocab,with_norm", [(151936, True), (1000, False), (1, True)])

@@ -310,9 +310,10 @@ KUDACUDA_API int kudacuda_qwen2_model_capture(void* model, uint64_t stream);
 /* Replay the captured step `steps` times back to back on `stream`. */
 KUDACUDA_API int kudacuda_qwen2_model_replay(void* model, int64_t steps, uint64_t stream);
 /* Time one kernel of the step in isolation: op 0 = qkv+rope, 1 = attention,
- * 2 = o_proj, 3 = gate/up, 4 = down, 5 = lm_head; `iters` launches cycling
- * over the layers (so weights are not cache resident), bracketed by HIP
- * events on `stream`; *avg_ms receives the mean launch duration. */
+ * 2 = o_proj, 3 = gate/up, 4 = down, 5 = lm_head; `iters` (1..4096) launches
+ * cycling over the layers (so weights are not cache resident) are captured in
+ * a hipGraph and replayed between two HIP events on `stream`; *avg_ms
+ * receives the mean launch duration. */
 KUDACUDA_API int kudacuda_qwen2_model_time_op(void* model, int64_t op, int64_t iters, uint64_t stream,
                                               float* avg_ms);
 KUDACUDA_API void kudacuda_qwen2_model_destroy(void* model);

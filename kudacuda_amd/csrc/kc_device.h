@@ -140,19 +140,51 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // ------------------------------------------------------------------ NF4 dots
+// v_bfe_u32 with a constant field: written as asm because the compiler
+// otherwise rewrites a chain of byte extracts of a pre-masked word back into a
+// shift and a mask per byte.
+template <int OFF>
+__device__ __forceinline__ uint32_t bfe8(uint32_t v) {
+    uint32_t r;
+    asm("v_bfe_u32 %0, %1, %2, 8" : "=v"(r) : "v"(v), "i"(OFF));
+    return r;
+}
+
+// Codebook values of the 32 codes of one chunk, gathered from the LDS table
+// before any arithmetic so the lookups overlap.  For each 32-bit word the
+// byte offsets code*4 of the high and low nibbles come from one shift and one
+// mask each ((w >> 2) & 0x3c..., (w << 2) & 0x3c...).
+__device__ __forceinline__ void nf4_gather32(const uint4 pk, const float* cb, float* cw) {
+    const uint32_t w[4] = {pk.x, pk.y, pk.z, pk.w};
+    const char* base = reinterpret_cast<const char*>(cb);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t hi4 = (w[i] >> 2) & 0x3c3c3c3cu;
+        const uint32_t lo4 = (w[i] << 2) & 0x3c3c3c3cu;
+        // one bitfield extract per code, offsets already scaled by 4
+        cw[8 * i + 0] = *reinterpret_cast<const float*>(base + bfe8<0>(hi4));
+        cw[8 * i + 1] = *reinterpret_cast<const float*>(base + bfe8<0>(lo4));
+        cw[8 * i + 2] = *reinterpret_cast<const float*>(base + bfe8<8>(hi4));
+        cw[8 * i + 3] = *reinterpret_cast<const float*>(base + bfe8<8>(lo4));
+        cw[8 * i + 4] = *reinterpret_cast<const float*>(base + bfe8<16>(hi4));
+        cw[8 * i + 5] = *reinterpret_cast<const float*>(base + bfe8<16>(lo4));
+        cw[8 * i + 6] = *reinterpret_cast<const float*>(base + bfe8<24>(hi4));
+        cw[8 * i + 7] = *reinterpret_cast<const float*>(base + bfe8<24>(lo4));
+    }
+}
+
 // Dot of one 32-element chunk with x[0..31] (already in fp32), before the
 // absmax multiply.  cb points at the codebook (LDS copy).
 __device__ __forceinline__ float nf4_chunk_dot_raw(const uint4 pk, const float* x, const float* cb) {
-    const uint32_t w[4] = {pk.x, pk.y, pk.z, pk.w};
+    float cw[32];
+    nf4_gather32(pk, cb, cw);
     float a[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         float acc = 0.0f;
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            const uint32_t byte = (w[i] >> (8 * b)) & 0xffu;
-            acc = fmaf(x[8 * i + 2 * b], cb[byte >> 4], acc);
-            acc = fmaf(x[8 * i + 2 * b + 1], cb[byte & 0xfu], acc);
+        for (int j = 0; j < 8; ++j) {
+            acc = fmaf(x[8 * i + j], cw[8 * i + j], acc);
         }
         a[i] = acc;
     }

@@ -23,7 +23,8 @@ namespace kc {
 namespace {
 
 constexpr int kLmThreads = 256;
-constexpr int kLmMaxBlocks = 1024;
+constexpr int kLmMaxBlocks = 768;  // 3072 waves: all resident at 3 waves/SIMD
+constexpr int kRing = 4;  // rows in flight per wave
 
 __device__ __forceinline__ bool better(float v, int32_t i, float bv, int32_t bi) {
     return v > bv || (v == bv && i < bi);
@@ -89,40 +90,46 @@ __global__ __launch_bounds__(kLmThreads) void lm_head_kernel(LmHeadArgs a) {
             }
         }
 
+        // ring of kRing rows per wave: row base + i*nwaves sits in slot i and is
+        // refilled with the row kRing*nwaves further on once consumed
         const int64_t nwaves = static_cast<int64_t>(gridDim.x) * (kLmThreads / 64);
-        int64_t row = static_cast<int64_t>(blockIdx.x) * (kLmThreads / 64) + wave;
-        uint4 w[4];
-        if (row < a.vocab) {
-            const uint4* src = reinterpret_cast<const uint4*>(a.weight + row * 2048);
+        const int64_t first = static_cast<int64_t>(blockIdx.x) * (kLmThreads / 64) + wave;
+        uint4 w[kRing][4];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                w[c] = src[lane + 64 * c];
-            }
-        }
-        while (row < a.vocab) {
-            const int64_t next = row + nwaves;
-            uint4 nw[4];
-            if (next < a.vocab) {
-                const uint4* src = reinterpret_cast<const uint4*>(a.weight + next * 2048);
+        for (int i = 0; i < kRing; ++i) {
+            const int64_t r = first + i * nwaves;
+            if (r < a.vocab) {
+                const uint4* src = reinterpret_cast<const uint4*>(a.weight + r * 2048);
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
-                    nw[c] = src[lane + 64 * c];
+                    w[i][c] = src[lane + 64 * c];
                 }
             }
-            const float sum = wave_sum(row_dot(w, xn));
-            const uint16_t lb = f32_to_bf16(sum);
-            const float v = bf16_to_f32(lb);
-            if (lane == 0 && a.logits != nullptr) {
-                a.logits[row] = lb;
-            }
-            if (better(v, static_cast<int32_t>(row), best, best_idx)) {
-                best = v;
-                best_idx = static_cast<int32_t>(row);
-            }
-            row = next;
+        }
+        for (int64_t base = first; base < a.vocab; base += kRing * nwaves) {
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                w[c] = nw[c];
+            for (int i = 0; i < kRing; ++i) {
+                const int64_t row = base + i * nwaves;
+                if (row < a.vocab) {
+                    const float sum = wave_sum(row_dot(w[i], xn));
+                    const int64_t rn = row + kRing * nwaves;
+                    if (rn < a.vocab) {
+                        const uint4* src = reinterpret_cast<const uint4*>(a.weight + rn * 2048);
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) {
+                            w[i][c] = src[lane + 64 * c];
+                        }
+                    }
+                    const uint16_t lb = f32_to_bf16(sum);
+                    const float v = bf16_to_f32(lb);
+                    if (lane == 0 && a.logits != nullptr) {
+                        a.logits[row] = lb;
+                    }
+                    if (better(v, static_cast<int32_t>(row), best, best_idx)) {
+                        best = v;
+                        best_idx = static_cast<int32_t>(row);
+                    }
+                }
             }
         }
         if (lane == 0) {

@@ -78,7 +78,63 @@ __device__ __forceinline__ void fetch_row(const Nf4RowsArgs& a, int m, int64_t r
     am = a.absmax[m][r * 32 + (lane >> 1)];
 }
 
+// Epilogue of one task (row pair) once both dots are reduced; every lane
+// holds d0/d1, lane 0 (and lane 1 for a GEMV pair) stores.
 template <typename T, RowMode MODE>
+__device__ __forceinline__ void row_epilogue(const Nf4RowsArgs& a, const RowPair& cur, float d0, float d1, int lane,
+                                             int64_t pos) {
+    if constexpr (MODE == RowMode::kGemv) {
+        if (lane < 2 && (lane == 0 || cur.has1)) {
+            const int64_t r = lane == 0 ? cur.r0 : cur.r1;
+            float v = lane == 0 ? d0 : d1;
+            if (a.bias[0] != nullptr) {
+                v = v + T::load(a.bias[0][r]);
+            }
+            if (a.residual != nullptr) {
+                v = T::load(a.residual[r]) + T::load(T::store(v));
+            }
+            a.out[0][r] = T::store(v);
+        }
+    } else if constexpr (MODE == RowMode::kSwiGlu) {
+        if (lane == 0) {
+            a.out[0][cur.r0] = T::store(silu_fixed(d0) * d1);
+        }
+    } else {
+        if (lane == 0) {
+            const int m = cur.m0;
+            const float v0 = d0 + T::load(a.bias[m][cur.r0]);
+            const float v1 = d1 + T::load(a.bias[m][cur.r1]);
+            if constexpr (MODE == RowMode::kQkv) {
+                a.out[m][cur.r0] = T::store(v0);
+                a.out[m][cur.r1] = T::store(v1);
+            } else {
+                float o0 = v0, o1 = v1;
+                if (m < 2) {
+                    const int64_t d = cur.r0 & 127;
+                    const float c = a.rope_cos[pos * 64 + d];
+                    const float s = a.rope_sin[pos * 64 + d];
+                    o0 = (v0 * c) - (v1 * s);
+                    o1 = (v1 * c) + (v0 * s);
+                }
+                if (m == 0) {
+                    a.out[0][cur.r0] = T::store(o0);
+                    a.out[0][cur.r1] = T::store(o1);
+                } else {
+                    uint16_t* cache = m == 1 ? a.kcache : a.vcache;
+                    const int64_t g = cur.r0 >> 7;
+                    const int64_t base = (g * a.capacity + pos) * 128;
+                    cache[base + (cur.r0 & 127)] = T::store(o0);
+                    cache[base + (cur.r1 & 127)] = T::store(o1);
+                }
+            }
+        }
+    }
+}
+
+// Each wave owns up to TPW tasks (task = gwave + i * nwaves) and requests
+// every row of them before it touches the activation vector, so a wave has
+// TPW x 2 KiB in flight and the whole launch pays one HBM round trip.
+template <typename T, RowMode MODE, int TPW>
 __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs a, int64_t ntasks) {
     __shared__ float cb[16];
     load_codebook_lds(cb);
@@ -86,7 +142,24 @@ __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs 
     const int wave = threadIdx.x >> 6;
     const int64_t waves_per_block = kRowsThreads / 64;
     const int64_t nwaves = static_cast<int64_t>(gridDim.x) * waves_per_block;
-    int64_t task = static_cast<int64_t>(blockIdx.x) * waves_per_block + wave;
+    const int64_t first = static_cast<int64_t>(blockIdx.x) * waves_per_block + wave;
+
+    RowPair tasks[TPW];
+    uint4 pk[TPW][2];
+    float am[TPW][2];
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+        const int64_t t = first + i * nwaves;
+        pk[i][0] = pk[i][1] = make_uint4(0, 0, 0, 0);
+        am[i][0] = am[i][1] = 0.0f;
+        if (t < ntasks) {
+            tasks[i] = map_task<MODE>(a, t);
+            fetch_row(a, tasks[i].m0, tasks[i].r0, lane, pk[i][0], am[i][0]);
+            if (tasks[i].has1) {
+                fetch_row(a, tasks[i].m1, tasks[i].r1, lane, pk[i][1], am[i][1]);
+            }
+        }
+    }
 
     int64_t pos = 0;
     if constexpr (MODE == RowMode::kQkvRope) {
@@ -101,19 +174,6 @@ __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs 
         int64_t tok = a.tokens[tpos];
         tok = tok < 0 ? 0 : (tok >= a.vocab ? a.vocab - 1 : tok);
         x = a.embed + tok * 2048;
-    }
-
-    // Issue the first task's weight loads before the norm so HBM latency
-    // overlaps the activation work.
-    RowPair cur;
-    uint4 pk0 = make_uint4(0, 0, 0, 0), pk1 = make_uint4(0, 0, 0, 0);
-    float am0 = 0.0f, am1 = 0.0f;
-    if (task < ntasks) {
-        cur = map_task<MODE>(a, task);
-        fetch_row(a, cur.m0, cur.r0, lane, pk0, am0);
-        if (cur.has1) {
-            fetch_row(a, cur.m1, cur.r1, lane, pk1, am1);
-        }
     }
 
     float xn[32];
@@ -137,81 +197,25 @@ __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs 
     }
     __syncthreads();  // codebook visible
 
-    while (task < ntasks) {
-        const int64_t next = task + nwaves;
-        RowPair nxt;
-        uint4 npk0 = make_uint4(0, 0, 0, 0), npk1 = make_uint4(0, 0, 0, 0);
-        float nam0 = 0.0f, nam1 = 0.0f;
-        if (next < ntasks) {
-            nxt = map_task<MODE>(a, next);
-            fetch_row(a, nxt.m0, nxt.r0, lane, npk0, nam0);
-            if (nxt.has1) {
-                fetch_row(a, nxt.m1, nxt.r1, lane, npk1, nam1);
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+        const int64_t t = first + i * nwaves;
+        if (t < ntasks) {
+            const float d0 = wave_sum(nf4_chunk_dot_raw(pk[i][0], xn, cb) * am[i][0]);
+            float d1 = 0.0f;
+            if (tasks[i].has1) {
+                d1 = wave_sum(nf4_chunk_dot_raw(pk[i][1], xn, cb) * am[i][1]);
             }
+            row_epilogue<T, MODE>(a, tasks[i], d0, d1, lane, pos);
         }
-
-        float d0 = wave_sum(nf4_chunk_dot_raw(pk0, xn, cb) * am0);
-        float d1 = 0.0f;
-        if (cur.has1) {
-            d1 = wave_sum(nf4_chunk_dot_raw(pk1, xn, cb) * am1);
-        }
-
-        if constexpr (MODE == RowMode::kGemv) {
-            if (lane < 2 && (lane == 0 || cur.has1)) {
-                const int64_t r = lane == 0 ? cur.r0 : cur.r1;
-                float v = lane == 0 ? d0 : d1;
-                if (a.bias[0] != nullptr) {
-                    v = v + T::load(a.bias[0][r]);
-                }
-                if (a.residual != nullptr) {
-                    v = T::load(a.residual[r]) + T::load(T::store(v));
-                }
-                a.out[0][r] = T::store(v);
-            }
-        } else if constexpr (MODE == RowMode::kSwiGlu) {
-            if (lane == 0) {
-                a.out[0][cur.r0] = T::store(silu_fixed(d0) * d1);
-            }
-        } else {
-            if (lane == 0) {
-                const int m = cur.m0;
-                const float v0 = d0 + T::load(a.bias[m][cur.r0]);
-                const float v1 = d1 + T::load(a.bias[m][cur.r1]);
-                if constexpr (MODE == RowMode::kQkv) {
-                    a.out[m][cur.r0] = T::store(v0);
-                    a.out[m][cur.r1] = T::store(v1);
-                } else {
-                    float o0 = v0, o1 = v1;
-                    if (m < 2) {
-                        const int64_t d = cur.r0 & 127;
-                        const float c = a.rope_cos[pos * 64 + d];
-                        const float s = a.rope_sin[pos * 64 + d];
-                        o0 = (v0 * c) - (v1 * s);
-                        o1 = (v1 * c) + (v0 * s);
-                    }
-                    if (m == 0) {
-                        a.out[0][cur.r0] = T::store(o0);
-                        a.out[0][cur.r1] = T::store(o1);
-                    } else {
-                        uint16_t* cache = m == 1 ? a.kcache : a.vcache;
-                        const int64_t g = cur.r0 >> 7;
-                        const int64_t base = (g * a.capacity + pos) * 128;
-                        cache[base + (cur.r0 & 127)] = T::store(o0);
-                        cache[base + (cur.r1 & 127)] = T::store(o1);
-                    }
-                }
-            }
-        }
-
-        task = next;
-        cur = nxt;
-        pk0 = npk0;
-        pk1 = npk1;
-        am0 = nam0;
-        am1 = nam1;
     }
 }
 
+// K = 11008 (NCHUNK = 344 chunks): a block of W = 6 waves covers one row
+// (chunk c -> wave c/64, lane c%64); each lane keeps its chunk's 32 inputs in
+// registers.  A block owns R rows per pass and requests all of their weights
+// before it reads the activation vector.  Row total = sum of the W wave sums
+// in wave order.
 template <typename T, int NCHUNK, int R>
 __global__ __launch_bounds__(64 * ((NCHUNK + 63) / 64)) void nf4_down_kernel(Nf4DownArgs a) {
     constexpr int W = (NCHUNK + 63) / 64;
@@ -222,6 +226,23 @@ __global__ __launch_bounds__(64 * ((NCHUNK + 63) / 64)) void nf4_down_kernel(Nf4
     const int wave = threadIdx.x >> 6;
     const int c = wave * 64 + lane;
     const bool valid = c < NCHUNK;
+    const int64_t row_bytes = static_cast<int64_t>(NCHUNK) * 16;
+    const int64_t row_blocks = NCHUNK / 2;
+
+    int64_t rbase = static_cast<int64_t>(blockIdx.x) * R;
+    uint4 pk[R];
+    float am[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        const int64_t r = rbase + i;
+        if (valid && r < a.rows) {
+            pk[i] = reinterpret_cast<const uint4*>(a.w + r * row_bytes)[c];
+            am[i] = a.absmax[r * row_blocks + (c >> 1)];
+        } else {
+            pk[i] = make_uint4(0, 0, 0, 0);
+            am[i] = 0.0f;
+        }
+    }
     float xv[32];
     if (valid) {
         const uint4* src = reinterpret_cast<const uint4*>(a.x + static_cast<int64_t>(c) * 32);
@@ -236,23 +257,7 @@ __global__ __launch_bounds__(64 * ((NCHUNK + 63) / 64)) void nf4_down_kernel(Nf4
         }
     }
     __syncthreads();
-    const int64_t row_bytes = static_cast<int64_t>(NCHUNK) * 16;
-    const int64_t row_blocks = NCHUNK / 2;
-    for (int64_t rbase = static_cast<int64_t>(blockIdx.x) * R; rbase < a.rows;
-         rbase += static_cast<int64_t>(gridDim.x) * R) {
-        uint4 pk[R];
-        float am[R];
-#pragma unroll
-        for (int i = 0; i < R; ++i) {
-            const int64_t r = rbase + i;
-            if (valid && r < a.rows) {
-                pk[i] = reinterpret_cast<const uint4*>(a.w + r * row_bytes)[c];
-                am[i] = a.absmax[r * row_blocks + (c >> 1)];
-            } else {
-                pk[i] = make_uint4(0, 0, 0, 0);
-                am[i] = 0.0f;
-            }
-        }
+    while (rbase < a.rows) {
 #pragma unroll
         for (int i = 0; i < R; ++i) {
             const int64_t r = rbase + i;
@@ -263,6 +268,17 @@ __global__ __launch_bounds__(64 * ((NCHUNK + 63) / 64)) void nf4_down_kernel(Nf4
             p = wave_sum(p);
             if (lane == 0) {
                 red[i][wave] = p;
+            }
+        }
+        const int64_t next = rbase + static_cast<int64_t>(gridDim.x) * R;
+        if (next < a.rows) {
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                const int64_t r = next + i;
+                if (valid && r < a.rows) {
+                    pk[i] = reinterpret_cast<const uint4*>(a.w + r * row_bytes)[c];
+                    am[i] = a.absmax[r * row_blocks + (c >> 1)];
+                }
             }
         }
         __syncthreads();
@@ -281,6 +297,7 @@ __global__ __launch_bounds__(64 * ((NCHUNK + 63) / 64)) void nf4_down_kernel(Nf4
             }
         }
         __syncthreads();
+        rbase = next;
     }
 }
 
@@ -343,6 +360,13 @@ __global__ __launch_bounds__(256) void nf4_dequantize_kernel(const uint8_t* pack
     }
 }
 
+template <typename T, RowMode MODE, int TPW>
+hipError_t launch_rows_tpw(const Nf4RowsArgs& a, int64_t ntasks, int64_t blocks, hipStream_t stream) {
+    hipLaunchKernelGGL((nf4_rows2048_kernel<T, MODE, TPW>), dim3(static_cast<unsigned>(blocks)), dim3(kRowsThreads),
+                       0, stream, a, ntasks);
+    return hipGetLastError();
+}
+
 template <typename T, RowMode MODE>
 hipError_t launch_rows_t(const Nf4RowsArgs& a, hipStream_t stream) {
     int64_t ntasks = 0;
@@ -356,15 +380,23 @@ hipError_t launch_rows_t(const Nf4RowsArgs& a, hipStream_t stream) {
     if (ntasks <= 0) {
         return hipSuccess;
     }
+    // at most 3072 waves (12 per CU on 256 CUs); every wave's tasks in flight
     const int64_t waves_per_block = kRowsThreads / 64;
-    int64_t blocks = (ntasks + waves_per_block - 1) / waves_per_block;
-    const int64_t max_blocks = 512;  // 2048 waves: 8 per CU on 256 CUs
-    if (blocks > max_blocks) {
-        blocks = max_blocks;
+    const int64_t max_waves = 3072;
+    int64_t tpw = (ntasks + max_waves - 1) / max_waves;
+    tpw = tpw <= 1 ? 1 : (tpw <= 2 ? 2 : (tpw <= 4 ? 4 : 8));
+    const int64_t waves = (ntasks + tpw - 1) / tpw;
+    const int64_t blocks = (waves + waves_per_block - 1) / waves_per_block;
+    switch (tpw) {
+        case 1:
+            return launch_rows_tpw<T, MODE, 1>(a, ntasks, blocks, stream);
+        case 2:
+            return launch_rows_tpw<T, MODE, 2>(a, ntasks, blocks, stream);
+        case 4:
+            return launch_rows_tpw<T, MODE, 4>(a, ntasks, blocks, stream);
+        default:
+            return launch_rows_tpw<T, MODE, 8>(a, ntasks, blocks, stream);
     }
-    hipLaunchKernelGGL((nf4_rows2048_kernel<T, MODE>), dim3(static_cast<unsigned>(blocks)), dim3(kRowsThreads), 0,
-                       stream, a, ntasks);
-    return hipGetLastError();
 }
 
 template <typename T>

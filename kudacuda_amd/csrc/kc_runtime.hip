@@ -1135,21 +1135,44 @@ int kudacuda_qwen2_model_time_op(void* raw_model, int64_t op, int64_t iters, uin
         return 1;
     }
     Handle* h = m->handle;
-    if (op < 0 || op > 5 || iters < 1 || avg_ms == nullptr) {
-        h->set_error("qwen2_model_time_op requires op 0..5, iters >= 1 and an output pointer");
+    if (op < 0 || op > 5 || iters < 1 || iters > 4096 || avg_ms == nullptr) {
+        h->set_error("qwen2_model_time_op requires op 0..5, iters 1..4096 and an output pointer");
         return 1;
     }
+    // The launches are captured into a graph and replayed, so the events see
+    // device time back to back rather than host launch gaps.
     hipStream_t s = as_stream(stream);
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
     hipEvent_t start = nullptr, stop = nullptr;
-    hipError_t status = hipEventCreate(&start);
+    hipError_t status = hipStreamBeginCapture(s, hipStreamCaptureModeGlobal);
+    hipError_t launch = hipSuccess;
+    for (int64_t i = 0; i < iters && status == hipSuccess && launch == hipSuccess; ++i) {
+        launch = kc::model_op(*m, static_cast<int>(op), i % m->num_layers, false, s);
+    }
+    if (status == hipSuccess) {
+        status = hipStreamEndCapture(s, &graph);
+    }
+    if (status == hipSuccess && launch != hipSuccess) {
+        status = launch;
+    }
+    if (status == hipSuccess) {
+        status = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    }
+    if (status == hipSuccess) {
+        status = hipGraphLaunch(exec, s);  // warm
+    }
+    if (status == hipSuccess) {
+        status = hipEventCreate(&start);
+    }
     if (status == hipSuccess) {
         status = hipEventCreate(&stop);
     }
     if (status == hipSuccess) {
         status = hipEventRecord(start, s);
     }
-    for (int64_t i = 0; i < iters && status == hipSuccess; ++i) {
-        status = kc::model_op(*m, static_cast<int>(op), i % m->num_layers, false, s);
+    if (status == hipSuccess) {
+        status = hipGraphLaunch(exec, s);
     }
     if (status == hipSuccess) {
         status = hipEventRecord(stop, s);
@@ -1166,6 +1189,12 @@ int kudacuda_qwen2_model_time_op(void* raw_model, int64_t op, int64_t iters, uin
     }
     if (stop != nullptr) {
         (void)hipEventDestroy(stop);
+    }
+    if (exec != nullptr) {
+        (void)hipGraphExecDestroy(exec);
+    }
+    if (graph != nullptr) {
+        (void)hipGraphDestroy(graph);
     }
     if (status == hipSuccess) {
         *avg_ms = ms / static_cast<float>(iters);

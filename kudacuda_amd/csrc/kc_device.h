@@ -242,10 +242,31 @@ __device__ __forceinline__ void load_norm_x2048(const uint16_t* __restrict__ x,
     }
 }
 
-__device__ __forceinline__ void load_codebook_lds(float* cb) {
-    if (threadIdx.x < 16) {
-        cb[threadIdx.x] = kNf4Codebook[threadIdx.x];
+// Codebook entry i (0..15) selected from immediates, so building the LDS copy
+// costs no memory round trip at kernel start.
+__device__ __forceinline__ float nf4_code_value(int i) {
+    constexpr float cb[16] = {
+        -0x1.000000p+0f, -0x1.647362p-1f, -0x1.0cd660p-1f, -0x1.946540p-2f,
+        -0x1.23449ap-2f, -0x1.7a6a7ep-3f, -0x1.74f0e2p-4f, 0x0.0p+0f,
+        0x1.45f5fep-4f,  0x1.4995c6p-3f,  0x1.f809bap-3f,  0x1.5a0674p-2f,
+        0x1.c34970p-2f,  0x1.200f56p-1f,  0x1.722766p-1f,  0x1.000000p+0f,
+    };
+    float v = cb[0];
+#pragma unroll
+    for (int k = 1; k < 16; ++k) {
+        v = i == k ? cb[k] : v;
     }
+    return v;
+}
+
+// Per-wave LDS copy of the codebook: lanes 0..15 write it and the same wave
+// reads it afterwards.  LDS operations of one wave complete in issue order,
+// so no block barrier is needed.
+__device__ __forceinline__ void wave_codebook_lds(float* cb, int lane) {
+    if (lane < 16) {
+        cb[lane] = nf4_code_value(lane);
+    }
+    __builtin_amdgcn_wave_barrier();
 }
 
 }  // namespace kc

@@ -63,73 +63,101 @@ __global__ __launch_bounds__(kLmThreads) void lm_head_kernel(LmHeadArgs a) {
     float best = -__builtin_huge_valf();
     int32_t best_idx = 0x7fffffff;
     if (active) {
-        // Final RMSNorm: inverse RMS over elements [32l, 32l+32) per lane,
-        // then the lane's dot elements 8(l + 64c) + j, normalised the same way.
-        float xs[32];
+        // Loads first, in a fixed order: the activation chunks (norm layout
+        // [32l, 32l+32) and dot layout 8(l + 64c) + j), gamma, then the first
+        // kRing rows of the ring, so the norm arithmetic overlaps the row
+        // loads and every wait is for a known prefix of the issued loads.
         const uint4* xv = reinterpret_cast<const uint4*>(a.x);
+        const bool has_gamma = a.gamma != nullptr;
+        const uint4* gv = reinterpret_cast<const uint4*>(has_gamma ? a.gamma : a.x);
+        uint4 xs_raw[4], xd_raw[4], g_raw[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            unpack8<Bf16>(xv[lane * 4 + i], xs + 8 * i);
+            xs_raw[i] = xv[lane * 4 + i];
         }
-        float r = 1.0f;
-        if (a.gamma != nullptr) {
-            r = inv_rms(wave_sum(sumsq32(xs)), 2048.0f, a.eps);
-        }
-        float xn[32];
-        const uint4* gv = reinterpret_cast<const uint4*>(a.gamma);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            unpack8<Bf16>(xv[lane + 64 * c], xn + 8 * c);
-            if (a.gamma != nullptr) {
-                float gf[8];
-                unpack8<Bf16>(gv[lane + 64 * c], gf);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    xn[8 * c + j] = (xn[8 * c + j] * r) * gf[j];
-                }
-            }
+            xd_raw[c] = xv[lane + 64 * c];
+            g_raw[c] = gv[lane + 64 * c];
         }
 
-        // ring of kRing rows per wave: row base + i*nwaves sits in slot i and is
-        // refilled with the row kRing*nwaves further on once consumed
+        // Ring of kRing rows per wave: row base + i*nwaves sits in slot i and is
+        // refilled with the row kRing*nwaves further on as soon as it has been
+        // consumed.  The loads are unconditional (rows past the end read the
+        // last row again, which stays in cache) so the loop body is straight
+        // line code and every dot waits only for its own slot's loads.
         const int64_t nwaves = static_cast<int64_t>(gridDim.x) * (kLmThreads / 64);
-        const int64_t first = static_cast<int64_t>(blockIdx.x) * (kLmThreads / 64) + wave;
+        // wave-uniform row numbers (scalar registers, scalar loop control)
+        const int64_t first = static_cast<int64_t>(blockIdx.x) * (kLmThreads / 64) +
+                              __builtin_amdgcn_readfirstlane(wave);
+        const int64_t last_row = a.vocab - 1;
+        const uint4* wbase = reinterpret_cast<const uint4*>(a.weight) + lane;
         uint4 w[kRing][4];
 #pragma unroll
         for (int i = 0; i < kRing; ++i) {
-            const int64_t r = first + i * nwaves;
-            if (r < a.vocab) {
-                const uint4* src = reinterpret_cast<const uint4*>(a.weight + r * 2048);
+            __builtin_amdgcn_sched_barrier(0);
+            const uint4* src = wbase + (first + i * nwaves < last_row ? first + i * nwaves : last_row) * 256;
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    w[i][c] = src[lane + 64 * c];
-                }
+            for (int c = 0; c < 4; ++c) {
+                w[i][c] = src[64 * c];
             }
         }
+        __builtin_amdgcn_sched_barrier(0);
+
+        // Final RMSNorm: inverse RMS over elements [32l, 32l+32) per lane,
+        // then the lane's dot elements normalised the same way.
+        float xs[32];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            unpack8<Bf16>(xs_raw[i], xs + 8 * i);
+        }
+        const float r = has_gamma ? inv_rms(wave_sum(sumsq32(xs)), 2048.0f, a.eps) : 1.0f;
+        float xn[32];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            unpack8<Bf16>(xd_raw[c], xn + 8 * c);
+            float gf[8];
+            unpack8<Bf16>(g_raw[c], gf);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                xn[8 * c + j] = has_gamma ? (xn[8 * c + j] * r) * gf[j] : xn[8 * c + j];
+            }
+        }
+
         for (int64_t base = first; base < a.vocab; base += kRing * nwaves) {
+            float sum[kRing];
+#pragma unroll
+            for (int i = 0; i < kRing; ++i) {
+                sum[i] = row_dot(w[i], xn);
+                const int64_t rn = base + (i + kRing) * nwaves;
+                const uint4* src = wbase + (rn < last_row ? rn : last_row) * 256;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    w[i][c] = src[64 * c];
+                }
+                // keep slot i's refill ahead of slot i+1's dot
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int i = 0; i < kRing; ++i) {
+                sum[i] = wave_sum(sum[i]);
+            }
+            // lane i (< kRing) stores slot i's logit: one store per pass
+            uint16_t lane_lb = 0;
 #pragma unroll
             for (int i = 0; i < kRing; ++i) {
                 const int64_t row = base + i * nwaves;
-                if (row < a.vocab) {
-                    const float sum = wave_sum(row_dot(w[i], xn));
-                    const int64_t rn = row + kRing * nwaves;
-                    if (rn < a.vocab) {
-                        const uint4* src = reinterpret_cast<const uint4*>(a.weight + rn * 2048);
-#pragma unroll
-                        for (int c = 0; c < 4; ++c) {
-                            w[i][c] = src[lane + 64 * c];
-                        }
-                    }
-                    const uint16_t lb = f32_to_bf16(sum);
-                    const float v = bf16_to_f32(lb);
-                    if (lane == 0 && a.logits != nullptr) {
-                        a.logits[row] = lb;
-                    }
-                    if (better(v, static_cast<int32_t>(row), best, best_idx)) {
-                        best = v;
-                        best_idx = static_cast<int32_t>(row);
-                    }
+                const uint16_t lb = f32_to_bf16(sum[i]);
+                const float v = bf16_to_f32(lb);
+                lane_lb = lane == i ? lb : lane_lb;
+                if (row < a.vocab && better(v, static_cast<int32_t>(row), best, best_idx)) {
+                    best = v;
+                    best_idx = static_cast<int32_t>(row);
                 }
+            }
+            const int64_t lane_row = base + lane * nwaves;
+            if (a.logits != nullptr && lane < kRing && lane_row < a.vocab) {
+                a.logits[lane_row] = lane_lb;
             }
         }
         if (lane == 0) {

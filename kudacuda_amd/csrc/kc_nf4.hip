@@ -78,20 +78,52 @@ __device__ __forceinline__ void fetch_row(const Nf4RowsArgs& a, int m, int64_t r
     am = a.absmax[m][r * 32 + (lane >> 1)];
 }
 
+// Small per-task operands of the epilogue (bias, residual, rotary
+// cos/sin), loaded with the weights so the epilogue itself never waits on
+// memory.  Every lane loads the same addresses (one request per wave); lane 0
+// (and lane 1 for a GEMV pair) uses them.
+struct Epi {
+    uint16_t b0 = 0, b1 = 0;  // bias (GEMV: lane's bias) raw 16-bit
+    uint16_t res = 0;         // GEMV residual of the lane's row
+    float c = 1.0f, s = 0.0f; // rotary cos/sin
+};
+
+template <typename T, RowMode MODE>
+__device__ __forceinline__ Epi fetch_epilogue(const Nf4RowsArgs& a, const RowPair& p, int lane, int64_t pos) {
+    Epi e;
+    if constexpr (MODE == RowMode::kGemv) {
+        const int64_t r = (lane == 1 && p.has1) ? p.r1 : p.r0;
+        // null operands read x[0] instead (always valid) and are ignored
+        const uint16_t* bias = a.bias[0] != nullptr ? a.bias[0] + r : a.x;
+        const uint16_t* res = a.residual != nullptr ? a.residual + r : a.x;
+        e.b0 = *bias;
+        e.res = *res;
+    } else if constexpr (MODE == RowMode::kQkv || MODE == RowMode::kQkvRope) {
+        e.b0 = a.bias[p.m0][p.r0];
+        e.b1 = a.bias[p.m0][p.r1];
+        if constexpr (MODE == RowMode::kQkvRope) {
+            const int64_t d = p.r0 & 127;
+            e.c = a.rope_cos[pos * 64 + d];
+            e.s = a.rope_sin[pos * 64 + d];
+        }
+    }
+    return e;
+}
+
 // Epilogue of one task (row pair) once both dots are reduced; every lane
 // holds d0/d1, lane 0 (and lane 1 for a GEMV pair) stores.
 template <typename T, RowMode MODE>
-__device__ __forceinline__ void row_epilogue(const Nf4RowsArgs& a, const RowPair& cur, float d0, float d1, int lane,
-                                             int64_t pos) {
+__device__ __forceinline__ void row_epilogue(const Nf4RowsArgs& a, const RowPair& cur, const Epi& e, float d0,
+                                             float d1, int lane, int64_t pos) {
     if constexpr (MODE == RowMode::kGemv) {
         if (lane < 2 && (lane == 0 || cur.has1)) {
             const int64_t r = lane == 0 ? cur.r0 : cur.r1;
             float v = lane == 0 ? d0 : d1;
             if (a.bias[0] != nullptr) {
-                v = v + T::load(a.bias[0][r]);
+                v = v + T::load(e.b0);
             }
             if (a.residual != nullptr) {
-                v = T::load(a.residual[r]) + T::load(T::store(v));
+                v = T::load(e.res) + T::load(T::store(v));
             }
             a.out[0][r] = T::store(v);
         }
@@ -102,19 +134,16 @@ __device__ __forceinline__ void row_epilogue(const Nf4RowsArgs& a, const RowPair
     } else {
         if (lane == 0) {
             const int m = cur.m0;
-            const float v0 = d0 + T::load(a.bias[m][cur.r0]);
-            const float v1 = d1 + T::load(a.bias[m][cur.r1]);
+            const float v0 = d0 + T::load(e.b0);
+            const float v1 = d1 + T::load(e.b1);
             if constexpr (MODE == RowMode::kQkv) {
                 a.out[m][cur.r0] = T::store(v0);
                 a.out[m][cur.r1] = T::store(v1);
             } else {
                 float o0 = v0, o1 = v1;
                 if (m < 2) {
-                    const int64_t d = cur.r0 & 127;
-                    const float c = a.rope_cos[pos * 64 + d];
-                    const float s = a.rope_sin[pos * 64 + d];
-                    o0 = (v0 * c) - (v1 * s);
-                    o1 = (v1 * c) + (v0 * s);
+                    o0 = (v0 * e.c) - (v1 * e.s);
+                    o1 = (v1 * e.c) + (v0 * e.s);
                 }
                 if (m == 0) {
                     a.out[0][cur.r0] = T::store(o0);
@@ -131,35 +160,20 @@ __device__ __forceinline__ void row_epilogue(const Nf4RowsArgs& a, const RowPair
     }
 }
 
-// Each wave owns up to TPW tasks (task = gwave + i * nwaves) and requests
-// every row of them before it touches the activation vector, so a wave has
-// TPW x 2 KiB in flight and the whole launch pays one HBM round trip.
+// Each wave owns up to TPW tasks (task = gwave + i * nwaves).  Loads are
+// issued in one fixed order before any arithmetic: activation and norm
+// weight, epilogue operands, then every row of every task (tasks past the end
+// re-read the last task's rows and are discarded).  Vector memory returns in
+// issue order, so the norm waits only for the small vectors while the rows
+// stream in, and each task's dot waits only for its own rows.
 template <typename T, RowMode MODE, int TPW>
 __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs a, int64_t ntasks) {
-    __shared__ float cb[16];
-    load_codebook_lds(cb);
+    __shared__ float cb_all[kRowsThreads / 64][16];
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t waves_per_block = kRowsThreads / 64;
     const int64_t nwaves = static_cast<int64_t>(gridDim.x) * waves_per_block;
     const int64_t first = static_cast<int64_t>(blockIdx.x) * waves_per_block + wave;
-
-    RowPair tasks[TPW];
-    uint4 pk[TPW][2];
-    float am[TPW][2];
-#pragma unroll
-    for (int i = 0; i < TPW; ++i) {
-        const int64_t t = first + i * nwaves;
-        pk[i][0] = pk[i][1] = make_uint4(0, 0, 0, 0);
-        am[i][0] = am[i][1] = 0.0f;
-        if (t < ntasks) {
-            tasks[i] = map_task<MODE>(a, t);
-            fetch_row(a, tasks[i].m0, tasks[i].r0, lane, pk[i][0], am[i][0]);
-            if (tasks[i].has1) {
-                fetch_row(a, tasks[i].m1, tasks[i].r1, lane, pk[i][1], am[i][1]);
-            }
-        }
-    }
 
     int64_t pos = 0;
     if constexpr (MODE == RowMode::kQkvRope) {
@@ -175,16 +189,77 @@ __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs 
         tok = tok < 0 ? 0 : (tok >= a.vocab ? a.vocab - 1 : tok);
         x = a.embed + tok * 2048;
     }
+    const bool has_gamma = a.gamma != nullptr;
+    const uint4* xv = reinterpret_cast<const uint4*>(x) + lane * 4;
+    const uint4* gv = reinterpret_cast<const uint4*>(has_gamma ? a.gamma : x) + lane * 4;
+    uint4 xr[4], gr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        xr[i] = xv[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        gr[i] = gv[i];
+    }
 
+    RowPair tasks[TPW];
+    Epi epi[TPW];
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+        const int64_t t = first + i * nwaves;
+        tasks[i] = map_task<MODE>(a, t < ntasks ? t : ntasks - 1);
+        epi[i] = fetch_epilogue<T, MODE>(a, tasks[i], lane, pos);
+    }
+    uint4 pk[TPW][2];
+    float am[TPW][2];
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+        __builtin_amdgcn_sched_barrier(0);
+        fetch_row(a, tasks[i].m0, tasks[i].r0, lane, pk[i][0], am[i][0]);
+        fetch_row(a, tasks[i].m1, tasks[i].has1 ? tasks[i].r1 : tasks[i].r0, lane, pk[i][1], am[i][1]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    float* cb = cb_all[wave];
+    wave_codebook_lds(cb, lane);
+
+    // RMSNorm of the lane's 32 elements against the whole vector
     float xn[32];
-    load_norm_x2048<T>(x, a.gamma, a.eps, lane, xn);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        unpack8<T>(xr[i], xn + 8 * i);
+    }
+    if (has_gamma) {
+        const float r = inv_rms(wave_sum(sumsq32(xn)), 2048.0f, a.eps);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float g[8];
+            unpack8<T>(gr[i], g);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                xn[8 * i + j] = (xn[8 * i + j] * r) * g[j];
+            }
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+        const float d0 = wave_sum(nf4_chunk_dot_raw(pk[i][0], xn, cb) * am[i][0]);
+        float d1 = 0.0f;
+        if (tasks[i].has1) {
+            d1 = wave_sum(nf4_chunk_dot_raw(pk[i][1], xn, cb) * am[i][1]);
+        }
+        if (first + i * nwaves < ntasks) {
+            row_epilogue<T, MODE>(a, tasks[i], epi[i], d0, d1, lane, pos);
+        }
+    }
+
     if (blockIdx.x == 0 && wave == 0) {
         if (a.hidden_out != nullptr) {
-            const uint4* src = reinterpret_cast<const uint4*>(x) + lane * 4;
             uint4* dst = reinterpret_cast<uint4*>(a.hidden_out) + lane * 4;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                dst[i] = src[i];
+                dst[i] = xr[i];
             }
         }
         if (a.norm_out != nullptr) {
@@ -195,109 +270,78 @@ __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs 
             }
         }
     }
-    __syncthreads();  // codebook visible
-
-#pragma unroll
-    for (int i = 0; i < TPW; ++i) {
-        const int64_t t = first + i * nwaves;
-        if (t < ntasks) {
-            const float d0 = wave_sum(nf4_chunk_dot_raw(pk[i][0], xn, cb) * am[i][0]);
-            float d1 = 0.0f;
-            if (tasks[i].has1) {
-                d1 = wave_sum(nf4_chunk_dot_raw(pk[i][1], xn, cb) * am[i][1]);
-            }
-            row_epilogue<T, MODE>(a, tasks[i], d0, d1, lane, pos);
-        }
-    }
 }
 
-// K = 11008 (NCHUNK = 344 chunks): a block of W = 6 waves covers one row
+// K = 11008 (NCHUNK = 344 chunks): a block of W = 6 waves covers R rows
 // (chunk c -> wave c/64, lane c%64); each lane keeps its chunk's 32 inputs in
-// registers.  A block owns R rows per pass and requests all of their weights
-// before it reads the activation vector.  Row total = sum of the W wave sums
-// in wave order.
+// registers.  Loads in issue order: activation chunk, residuals of the
+// block's rows, then the R rows (lanes past the last chunk re-read it and
+// contribute 0).  Row total = sum of the W wave sums in wave order.
 template <typename T, int NCHUNK, int R>
 __global__ __launch_bounds__(64 * ((NCHUNK + 63) / 64)) void nf4_down_kernel(Nf4DownArgs a) {
     constexpr int W = (NCHUNK + 63) / 64;
-    __shared__ float cb[16];
+    __shared__ float cb_all[W][16];
     __shared__ float red[R][W];
-    load_codebook_lds(cb);
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = wave * 64 + lane;
     const bool valid = c < NCHUNK;
-    const int64_t row_bytes = static_cast<int64_t>(NCHUNK) * 16;
+    const int cc = valid ? c : NCHUNK - 1;
+    const int64_t row_chunks = NCHUNK;
     const int64_t row_blocks = NCHUNK / 2;
+    const int64_t rbase = static_cast<int64_t>(blockIdx.x) * R;
+    const int64_t last_row = a.rows - 1;
 
-    int64_t rbase = static_cast<int64_t>(blockIdx.x) * R;
+    uint4 xr[4];
+    const uint4* src = reinterpret_cast<const uint4*>(a.x) + static_cast<int64_t>(cc) * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        xr[i] = src[i];
+    }
+    // thread t < R finishes row rbase + t
+    const int64_t my_row = rbase + (threadIdx.x % R) < last_row ? rbase + (threadIdx.x % R) : last_row;
+    const uint16_t res = a.residual != nullptr ? a.residual[my_row] : static_cast<uint16_t>(0);
+
     uint4 pk[R];
     float am[R];
+    const uint4* wv = reinterpret_cast<const uint4*>(a.w) + cc;
 #pragma unroll
     for (int i = 0; i < R; ++i) {
-        const int64_t r = rbase + i;
-        if (valid && r < a.rows) {
-            pk[i] = reinterpret_cast<const uint4*>(a.w + r * row_bytes)[c];
-            am[i] = a.absmax[r * row_blocks + (c >> 1)];
-        } else {
-            pk[i] = make_uint4(0, 0, 0, 0);
-            am[i] = 0.0f;
-        }
+        __builtin_amdgcn_sched_barrier(0);
+        const int64_t r = rbase + i < last_row ? rbase + i : last_row;
+        pk[i] = wv[r * row_chunks];
+        am[i] = a.absmax[r * row_blocks + (cc >> 1)];
     }
+    __builtin_amdgcn_sched_barrier(0);
+
+    float* cb = cb_all[wave];
+    wave_codebook_lds(cb, lane);
     float xv[32];
-    if (valid) {
-        const uint4* src = reinterpret_cast<const uint4*>(a.x + static_cast<int64_t>(c) * 32);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            unpack8<T>(src[i], xv + 8 * i);
-        }
-    } else {
+    for (int i = 0; i < 4; ++i) {
+        unpack8<T>(xr[i], xv + 8 * i);
+    }
+
 #pragma unroll
-        for (int j = 0; j < 32; ++j) {
-            xv[j] = 0.0f;
+    for (int i = 0; i < R; ++i) {
+        float p = nf4_chunk_dot_raw(pk[i], xv, cb) * am[i];
+        p = wave_sum(valid ? p : 0.0f);
+        if (lane == 0) {
+            red[i][wave] = p;
         }
     }
     __syncthreads();
-    while (rbase < a.rows) {
+    if (threadIdx.x < R && rbase + threadIdx.x < a.rows) {
+        const int64_t r = rbase + threadIdx.x;
+        float s = red[threadIdx.x][0];
 #pragma unroll
-        for (int i = 0; i < R; ++i) {
-            const int64_t r = rbase + i;
-            float p = 0.0f;
-            if (valid && r < a.rows) {
-                p = nf4_chunk_dot_raw(pk[i], xv, cb) * am[i];
-            }
-            p = wave_sum(p);
-            if (lane == 0) {
-                red[i][wave] = p;
-            }
+        for (int w = 1; w < W; ++w) {
+            s = s + red[threadIdx.x][w];
         }
-        const int64_t next = rbase + static_cast<int64_t>(gridDim.x) * R;
-        if (next < a.rows) {
-#pragma unroll
-            for (int i = 0; i < R; ++i) {
-                const int64_t r = next + i;
-                if (valid && r < a.rows) {
-                    pk[i] = reinterpret_cast<const uint4*>(a.w + r * row_bytes)[c];
-                    am[i] = a.absmax[r * row_blocks + (c >> 1)];
-                }
-            }
+        if (a.residual != nullptr) {
+            s = T::load(res) + T::load(T::store(s));
         }
-        __syncthreads();
-        if (threadIdx.x < R) {
-            const int64_t r = rbase + threadIdx.x;
-            if (r < a.rows) {
-                float s = red[threadIdx.x][0];
-#pragma unroll
-                for (int w = 1; w < W; ++w) {
-                    s = s + red[threadIdx.x][w];
-                }
-                if (a.residual != nullptr) {
-                    s = T::load(a.residual[r]) + T::load(T::store(s));
-                }
-                a.out[r] = T::store(s);
-            }
-        }
-        __syncthreads();
-        rbase = next;
+        a.out[r] = T::store(s);
     }
 }
 

@@ -1,0 +1,89 @@
+"""Pins of the oracle's split-KV grouped-query decode attention
+(16 query heads, 2 KV heads, head_dim 128)."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from oracle.reference import compare_values, gqa_f64
+from tests import _kat
+
+F = np.float32
+SCALE = 1.0 / math.sqrt(128.0)
+
+
+def test_reference_gqa_smoke_fixture():
+    q, k, v, tol = _kat.gqa_smoke_case(37)
+    got = O.f16_to_f32(O.gqa(q, k, v, 37, dtype="f16"))
+    want = gqa_f64(O.f16_to_f32(q), O.f16_to_f32(k), O.f16_to_f32(v), 37, SCALE)
+    assert np.abs(got - want).max() <= tol
+
+
+def test_reference_gqa_workspace_fixture():
+    q, k, v, lens, tol = _kat.gqa_workspace_case()
+    for kv_len in lens:
+        got = O.f16_to_f32(O.gqa(q, k, v, kv_len, dtype="f16"))
+        want = gqa_f64(O.f16_to_f32(q), O.f16_to_f32(k), O.f16_to_f32(v), kv_len, SCALE)
+        assert np.abs(got - want).max() <= tol, kv_len
+
+
+@pytest.mark.parametrize("kv_len", [1, 7, 128, 512, 585, 1024, 2048])
+def test_random_inputs_at_the_correctness_tool_lengths(kv_len):
+    # tools/correctness/run_qwen2_gqa_check.py:41-47,94-99: seed 20260824, atol = rtol = 3.5e-3
+    rng = np.random.default_rng([20260824, kv_len])
+    q = O.f32_to_bf16(rng.standard_normal(2048).astype(F))
+    k = O.f32_to_bf16(rng.standard_normal((2, kv_len, 128)).astype(F))
+    v = O.f32_to_bf16(rng.standard_normal((2, kv_len, 128)).astype(F))
+    got = O.bf16_to_f32(O.gqa(q, k, v, kv_len))
+    want = gqa_f64(O.bf16_to_f32(q), O.bf16_to_f32(k), O.bf16_to_f32(v), kv_len, SCALE)
+    # bf16 output: the comparison tolerance of the tool widened to bf16 rounding
+    result = compare_values(got.tolist(), want.tolist(), atol=3.5e-3, rtol=2.0 ** -8)
+    assert result["passed"], result
+
+
+def test_single_token_returns_the_value_row_exactly():
+    rng = np.random.default_rng(2)
+    q = O.f32_to_bf16(rng.standard_normal(2048).astype(F))
+    k = O.f32_to_bf16(rng.standard_normal((2, 64, 128)).astype(F))
+    v = O.f32_to_bf16(rng.standard_normal((2, 64, 128)).astype(F))
+    out = O.gqa(q, k, v, 1).reshape(16, 128)
+    for h in range(16):
+        assert out[h].tobytes() == v[h // 8, 0].tobytes()
+
+
+def test_identical_keys_average_the_values():
+    rng = np.random.default_rng(4)
+    kv_len = 300
+    q = O.f32_to_bf16(rng.standard_normal(2048).astype(F))
+    row = O.f32_to_bf16(rng.standard_normal(128).astype(F))
+    k = np.broadcast_to(row, (2, kv_len, 128)).copy()
+    v = O.f32_to_bf16(rng.standard_normal((2, kv_len, 128)).astype(F))
+    out = O.bf16_to_f32(O.gqa(q, k, v, kv_len)).reshape(16, 128)
+    mean = O.bf16_to_f32(v).astype(np.float64)[:, :kv_len].mean(axis=1)
+    for h in range(16):
+        assert np.all(np.abs(out[h] - mean[h // 8]) <= 2.0 ** -8 * np.abs(mean[h // 8]) + 1e-5)
+
+
+@pytest.mark.parametrize("chunk", [128, 256, 512, 1024])
+def test_split_size_changes_only_rounding(chunk):
+    rng = np.random.default_rng(6)
+    kv_len = 2000
+    q = O.f32_to_bf16(rng.standard_normal(2048).astype(F))
+    k = O.f32_to_bf16(rng.standard_normal((2, 2048, 128)).astype(F))
+    v = O.f32_to_bf16(rng.standard_normal((2, 2048, 128)).astype(F))
+    got = O.bf16_to_f32(O.gqa(q, k, v, kv_len, chunk=chunk))
+    want = gqa_f64(O.bf16_to_f32(q), O.bf16_to_f32(k), O.bf16_to_f32(v), kv_len, SCALE)
+    assert np.all(np.abs(got - want) <= 2.0 ** -7 * np.abs(want) + 2e-4)
+
+
+def test_planted_wrong_group_mapping_fails():
+    """Feeding the KV heads swapped is what an oracle with group = h % 2 would see."""
+
+    q, k, v, tol = _kat.gqa_smoke_case(37)
+    got = O.f16_to_f32(O.gqa(q, k[::-1].copy(), v[::-1].copy(), 37, dtype="f16"))
+    want = gqa_f64(O.f16_to_f32(q), O.f16_to_f32(k), O.f16_to_f32(v), 37, SCALE)
+    assert np.abs(got - want).max() > tol

@@ -41,6 +41,17 @@ PROMPT_LEN = 64
 NEW_TOKENS = 128
 KV_BUCKET = 2048
 GOLDEN = ROOT / "tests" / "golden" / "decode_qwen25_3b_nf4.json"
+TRAFFIC = ROOT / "profiles" / "traffic.json"
+
+
+def measured_traffic(kernel: str) -> int | None:
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 PMC
+    FETCH_SIZE/WRITE_SIZE runs (copy-kernel scaled), or None if not measured."""
+
+    if not TRAFFIC.exists():
+        return None
+    entry = json.loads(TRAFFIC.read_text()).get("kernels", {}).get(kernel)
+    return None if entry is None else int(entry["hbm_bytes"])
 
 
 def op_bytes(cfg, vocab: int, kv_len: int) -> dict[str, int]:
@@ -216,7 +227,7 @@ def main(argv: list[str] | None = None) -> int:
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(dominant),
         },
         "step_hbm_gbs": round(step_bytes(cfg, cfg.vocab, kv_len) * value / 1e9, 1),
         "per_kernel": op_report,

@@ -139,6 +139,27 @@ __device__ __forceinline__ float wave_sum(float v) {
     return group16_sum(v);
 }
 
+// -------------------------------------------------- cross-block exchange
+// Blocks of one launch that hand results to a "last block" (ticket pattern)
+// exchange only a few words.  A device-scope fence would write back and
+// invalidate the whole L2 of the XCD (the XCDs' L2 caches are not coherent
+// with each other), which costs microseconds per block.  Instead the
+// exchanged words are written and read with agent-scope atomic stores/loads,
+// which are coherent across XCDs, and every wave waits for its own stores to
+// complete before the block increments the ticket.
+__device__ __forceinline__ void store_agent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_agent(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Wait until this wave's vector memory operations (the exchange stores) have
+// completed; call before the barrier that precedes the ticket increment.
+__device__ __forceinline__ void wait_own_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 // ------------------------------------------------------------------ NF4 dots
 // v_bfe_u32 with a constant field: written as asm because the compiler
 // otherwise rewrites a chain of byte extracts of a pre-masked word back into a

@@ -320,18 +320,19 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a, int
         const int hl = half * 4 + threadIdx.x / kDim;
         const int d = threadIdx.x % kDim;
         float* dst = part + ((g * kHeadsPerGroup + hl) * a.max_splits + s) * kPartialStride;
-        dst[2 + d] = av_out[half];
+        store_agent(dst + 2 + d, av_out[half]);
         if (d == 0) {
-            dst[0] = s_M[hl];
-            dst[1] = s_L[hl];
+            store_agent(dst, s_M[hl]);
+            store_agent(dst + 1, s_L[hl]);
         }
     }
     if (merge_mode == 2) {
         return;  // gqa_merge_kernel follows
     }
 
-    // ---- ticket: the last block of this KV head merges all splits
-    __threadfence();
+    // ---- ticket: the last block of this KV head merges all splits (the
+    // partials travel through agent-scope atomic stores/loads, no fences)
+    wait_own_stores();
     __syncthreads();
     if (threadIdx.x == 0) {
         const uint32_t prev = atomicAdd(a.counters + g, 1u);
@@ -341,9 +342,8 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a, int
     if (s_last == 0) {
         return;
     }
-    __threadfence();
     if (threadIdx.x == 0) {
-        a.counters[g] = 0u;
+        store_agent(a.counters + g, 0u);
     }
     if (threadIdx.x < kHeadsPerGroup * kInKernelSplits) {
         const int hl = threadIdx.x / kInKernelSplits;
@@ -352,7 +352,7 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a, int
         float mv[kInKernelSplits];
 #pragma unroll
         for (int x = 0; x < kInKernelSplits; ++x) {
-            mv[x] = x < nsplit ? src[x * kPartialStride] : kNegInf;
+            mv[x] = x < nsplit ? load_agent(src + x * kPartialStride) : kNegInf;
         }
         float M = kNegInf;
 #pragma unroll
@@ -360,7 +360,7 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a, int
             M = fmaxf(M, mv[x]);
         }
         if (ss < nsplit) {
-            s_sw[ss][hl] = exp2_fixed(src[ss * kPartialStride] - M);
+            s_sw[ss][hl] = exp2_fixed(load_agent(src + ss * kPartialStride) - M);
         }
     }
     __syncthreads();
@@ -370,7 +370,7 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a, int
         float lv[kInKernelSplits];
 #pragma unroll
         for (int x = 0; x < kInKernelSplits; ++x) {
-            lv[x] = x < nsplit ? src[x * kPartialStride + 1] : 0.0f;
+            lv[x] = x < nsplit ? load_agent(src + x * kPartialStride + 1) : 0.0f;
         }
         float lt = 0.0f;
 #pragma unroll
@@ -391,7 +391,7 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a, int
         float vals[kInKernelSplits];
 #pragma unroll
         for (int x = 0; x < kInKernelSplits; ++x) {
-            vals[x] = x < nsplit ? src[x * kPartialStride] : 0.0f;
+            vals[x] = x < nsplit ? load_agent(src + x * kPartialStride) : 0.0f;
         }
         float o = 0.0f;
 #pragma unroll

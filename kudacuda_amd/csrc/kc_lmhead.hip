@@ -172,12 +172,13 @@ __global__ __launch_bounds__(kLmThreads) void lm_head_kernel(LmHeadArgs a) {
                     best_idx = s_idx[i];
                 }
             }
-            a.block_best[2 * blockIdx.x] = best;
-            a.block_best[2 * blockIdx.x + 1] = __int_as_float(best_idx);
+            store_agent(a.block_best + 2 * blockIdx.x, best);
+            store_agent(a.block_best + 2 * blockIdx.x + 1, __int_as_float(best_idx));
         }
     }
 
-    __threadfence();
+    // block winners travel through agent-scope atomic stores/loads (no fences)
+    wait_own_stores();
     __syncthreads();
     if (threadIdx.x == 0) {
         const uint32_t prev = atomicAdd(a.counter, 1u);
@@ -187,13 +188,12 @@ __global__ __launch_bounds__(kLmThreads) void lm_head_kernel(LmHeadArgs a) {
     if (s_last == 0) {
         return;
     }
-    __threadfence();
     if (active) {
         best = -__builtin_huge_valf();
         best_idx = 0x7fffffff;
         for (int b = threadIdx.x; b < static_cast<int>(gridDim.x); b += kLmThreads) {
-            const float v = a.block_best[2 * b];
-            const int32_t i = __float_as_int(a.block_best[2 * b + 1]);
+            const float v = load_agent(a.block_best + 2 * b);
+            const int32_t i = __float_as_int(load_agent(a.block_best + 2 * b + 1));
             if (better(v, i, best, best_idx)) {
                 best = v;
                 best_idx = i;
@@ -236,7 +236,7 @@ __global__ __launch_bounds__(kLmThreads) void lm_head_kernel(LmHeadArgs a) {
             }
             a.control[0] = next;
         }
-        a.counter[0] = 0u;
+        store_agent(a.counter, 0u);
     }
 }
 

@@ -85,7 +85,6 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a, int
     __shared__ float s_M[kHeadsPerGroup];
     __shared__ float s_L[kHeadsPerGroup];
     __shared__ float s_acc[kGroups][kHeadsPerGroup / 2][kDim];  // half the heads at a time
-    __shared__ float s_sw[kInKernelSplits][kHeadsPerGroup];
     __shared__ int s_last;
 
     const int g = blockIdx.y;
@@ -99,8 +98,14 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a, int
     const uint16_t* vbase = a.v + static_cast<int64_t>(g) * a.capacity * kDim + 8 * li;
     const int64_t t0 = s * C;
 
-    // Split 0 always exists once kv_len >= 1: its first rows (bounded by the
-    // capacity) are requested before kv_len is known.
+    // q does not depend on kv_len: request it first.  Split 0 always exists
+    // once kv_len >= 1, so its first rows (bounded by the capacity) are also
+    // requested before kv_len is known.
+    uint4 qr[kHeadsPerGroup];
+#pragma unroll
+    for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
+        qr[hl] = *reinterpret_cast<const uint4*>(a.q + (g * kHeadsPerGroup + hl) * kDim + 8 * li);
+    }
     uint4 kr[4], vr[4];
     int spec = 0;
     if (s == 0) {
@@ -117,8 +122,7 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a, int
     float q[kHeadsPerGroup][8];
 #pragma unroll
     for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
-        const uint4 v = *reinterpret_cast<const uint4*>(a.q + (g * kHeadsPerGroup + hl) * kDim + 8 * li);
-        unpack8<T>(v, q[hl]);
+        unpack8<T>(qr[hl], q[hl]);
     }
     // softmax state of head li lives in lane li (< 8) of each group
     float m_own = kNegInf, l_own = 0.0f;
@@ -345,122 +349,122 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a, int
     if (threadIdx.x == 0) {
         store_agent(a.counters + g, 0u);
     }
-    if (threadIdx.x < kHeadsPerGroup * kInKernelSplits) {
-        const int hl = threadIdx.x / kInKernelSplits;
-        const int ss = threadIdx.x % kInKernelSplits;
+    // One pass: every thread issues all the loads it needs (the split maxima
+    // and sums of its head and its element of every split's accumulator),
+    // then forms the weights exp2(m_s - M) itself and sums in split order.
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int idx = threadIdx.x + k * kGqaThreads;
+        const int hl = idx / kDim;
+        const int d = idx % kDim;
         const float* src = part + (g * kHeadsPerGroup + hl) * a.max_splits * kPartialStride;
-        float mv[kInKernelSplits];
+        float mv[kInKernelSplits], lv[kInKernelSplits], vv[kInKernelSplits];
 #pragma unroll
         for (int x = 0; x < kInKernelSplits; ++x) {
-            mv[x] = x < nsplit ? load_agent(src + x * kPartialStride) : kNegInf;
+            const bool live = x < nsplit;
+            mv[x] = live ? load_agent(src + x * kPartialStride) : kNegInf;
+            lv[x] = live ? load_agent(src + x * kPartialStride + 1) : 0.0f;
+            vv[x] = live ? load_agent(src + x * kPartialStride + 2 + d) : 0.0f;
         }
         float M = kNegInf;
 #pragma unroll
         for (int x = 0; x < kInKernelSplits; ++x) {
             M = fmaxf(M, mv[x]);
         }
-        if (ss < nsplit) {
-            s_sw[ss][hl] = exp2_fixed(load_agent(src + ss * kPartialStride) - M);
-        }
-    }
-    __syncthreads();
-    if (threadIdx.x < kHeadsPerGroup) {
-        const int hl = threadIdx.x;
-        const float* src = part + (g * kHeadsPerGroup + hl) * a.max_splits * kPartialStride;
-        float lv[kInKernelSplits];
-#pragma unroll
-        for (int x = 0; x < kInKernelSplits; ++x) {
-            lv[x] = x < nsplit ? load_agent(src + x * kPartialStride + 1) : 0.0f;
-        }
         float lt = 0.0f;
-#pragma unroll
-        for (int x = 0; x < kInKernelSplits; ++x) {
-            if (x < nsplit) {
-                lt = fmaf(lv[x], s_sw[x][hl], lt);
-            }
-        }
-        s_L[hl] = lt;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        const int idx = threadIdx.x + k * kGqaThreads;
-        const int hl = idx / kDim;
-        const int d = idx % kDim;
-        const float* src = part + (g * kHeadsPerGroup + hl) * a.max_splits * kPartialStride + 2 + d;
-        float vals[kInKernelSplits];
-#pragma unroll
-        for (int x = 0; x < kInKernelSplits; ++x) {
-            vals[x] = x < nsplit ? load_agent(src + x * kPartialStride) : 0.0f;
-        }
         float o = 0.0f;
 #pragma unroll
         for (int x = 0; x < kInKernelSplits; ++x) {
             if (x < nsplit) {
-                o = fmaf(vals[x], s_sw[x][hl], o);
+                const float w = exp2_fixed(mv[x] - M);
+                lt = fmaf(lv[x], w, lt);
+                o = fmaf(vv[x], w, o);
             }
         }
-        a.out[(g * kHeadsPerGroup + hl) * kDim + d] = T::store(o / s_L[hl]);
+        a.out[(g * kHeadsPerGroup + hl) * kDim + d] = T::store(o / lt);
     }
 }
 
-// grid (16 query heads, 128 / kMergeDims): M* over the splits (order-free
-// max), weights exp2(M_s - M*), then the split sums and the weighted acc
-// summed in split order from LDS-staged partials.
+// grid (16 query heads, 128 / kMergeDims).  One load pass: thread t brings
+// splits t, t+256, ... (max, sum and this block's 16-float slice of the
+// accumulator, as float4s) into LDS, all loads in flight together.  The
+// maximum over splits is an order-free reduction; the weights exp2(m_s - M)
+// and the two sums then run in split order, as in the in-kernel merge.
 template <typename T>
 __global__ __launch_bounds__(256) void gqa_merge_kernel(GqaArgs a) {
-    __shared__ float s_w[kMergeMaxSplits];
-    __shared__ float s_v[kMergeMaxSplits / 4][kMergeDims];  // one quarter of the splits at a time
-    __shared__ float s_red[256];
+    constexpr int kPerThread = kMergeMaxSplits / 256;
+    __shared__ float s_m[kMergeMaxSplits];
+    __shared__ float s_l[kMergeMaxSplits];
+    __shared__ __attribute__((aligned(16))) float s_v[kMergeMaxSplits][kMergeDims];
+    __shared__ float s_red[4];
     __shared__ float s_lt;
     const int h = blockIdx.x;
     const int d0 = blockIdx.y * kMergeDims;
     const int64_t L = read_kv_len(a);
-    const int64_t nsplit = (L + a.chunk - 1) / a.chunk;
+    const int nsplit = static_cast<int>((L + a.chunk - 1) / a.chunk);
     if (nsplit < 1) {
         return;
     }
     const float* src = a.partials + static_cast<int64_t>(h) * a.max_splits * kPartialStride;
-    float M = kNegInf;
-    for (int64_t x = threadIdx.x; x < nsplit; x += 256) {
-        M = fmaxf(M, src[x * kPartialStride]);
-    }
-    s_red[threadIdx.x] = M;
-    __syncthreads();
-    for (int o = 128; o >= 1; o >>= 1) {
-        if (threadIdx.x < o) {
-            s_red[threadIdx.x] = fmaxf(s_red[threadIdx.x], s_red[threadIdx.x + o]);
+    float mloc = kNegInf;
+    float mr[kPerThread], lr[kPerThread];
+    float4 vr[kPerThread][kMergeDims / 4];
+#pragma unroll
+    for (int i = 0; i < kPerThread; ++i) {
+        const int x = static_cast<int>(threadIdx.x) + 256 * i;
+        const int xs = x < nsplit ? x : 0;  // past the end: re-read split 0, unused
+        const float* row = src + static_cast<int64_t>(xs) * kPartialStride;
+        mr[i] = row[0];
+        lr[i] = row[1];
+#pragma unroll
+        for (int j = 0; j < kMergeDims / 4; ++j) {
+            const float* p = row + 2 + d0 + 4 * j;
+            vr[i][j] = make_float4(p[0], p[1], p[2], p[3]);
         }
-        __syncthreads();
     }
-    M = s_red[0];
-    for (int64_t x = threadIdx.x; x < nsplit; x += 256) {
-        s_w[x] = exp2_fixed(src[x * kPartialStride] - M);
+#pragma unroll
+    for (int i = 0; i < kPerThread; ++i) {
+        const int x = static_cast<int>(threadIdx.x) + 256 * i;
+        if (x < nsplit) {
+            s_m[x] = mr[i];
+            s_l[x] = lr[i];
+            mloc = fmaxf(mloc, mr[i]);
+#pragma unroll
+            for (int j = 0; j < kMergeDims / 4; ++j) {
+                *reinterpret_cast<float4*>(&s_v[x][4 * j]) = vr[i][j];
+            }
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        mloc = fmaxf(mloc, __shfl_xor(mloc, o, 64));
+    }
+    if ((threadIdx.x & 63) == 0) {
+        s_red[threadIdx.x >> 6] = mloc;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
+    const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    // weights in place of the maxima (each thread rewrites its own splits)
+#pragma unroll
+    for (int i = 0; i < kPerThread; ++i) {
+        const int x = static_cast<int>(threadIdx.x) + 256 * i;
+        if (x < nsplit) {
+            s_m[x] = exp2_fixed(mr[i] - M);
+        }
+    }
+    __syncthreads();
+    const int d = threadIdx.x;
+    if (d == kMergeDims) {
         float lt = 0.0f;
-        for (int64_t x = 0; x < nsplit; ++x) {
-            lt = fmaf(src[x * kPartialStride + 1], s_w[x], lt);
+        for (int x = 0; x < nsplit; ++x) {
+            lt = fmaf(s_l[x], s_m[x], lt);
         }
         s_lt = lt;
     }
     float o = 0.0f;
-    const int d = threadIdx.x;  // threads < kMergeDims accumulate
-    constexpr int64_t kTile = kMergeMaxSplits / 4;
-    for (int64_t x0 = 0; x0 < nsplit; x0 += kTile) {
-        const int64_t n = (nsplit - x0 < kTile) ? nsplit - x0 : kTile;
-        __syncthreads();
-        for (int64_t e = threadIdx.x; e < n * kMergeDims; e += 256) {
-            const int64_t x = e / kMergeDims;
-            const int dd = static_cast<int>(e % kMergeDims);
-            s_v[x][dd] = src[(x0 + x) * kPartialStride + 2 + d0 + dd];
-        }
-        __syncthreads();
-        if (d < kMergeDims) {
-            for (int64_t x = 0; x < n; ++x) {
-                o = fmaf(s_v[x][d], s_w[x0 + x], o);
-            }
+    if (d < kMergeDims) {
+        for (int x = 0; x < nsplit; ++x) {
+            o = fmaf(s_v[x][d], s_m[x], o);
         }
     }
     __syncthreads();

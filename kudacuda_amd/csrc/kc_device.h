@@ -280,14 +280,14 @@ __device__ __forceinline__ float nf4_code_value(int i) {
     return v;
 }
 
-// Per-wave LDS copy of the codebook: lanes 0..15 write it and the same wave
-// reads it afterwards.  LDS operations of one wave complete in issue order,
-// so no block barrier is needed.
-__device__ __forceinline__ void wave_codebook_lds(float* cb, int lane) {
-    if (lane < 16) {
-        cb[lane] = nf4_code_value(lane);
+// Block-shared LDS copy of the codebook at a fixed LDS address (so every
+// lookup's base folds into the ds_read offset): threads 0..15 write it; the
+// caller publishes it with a block barrier placed after its global loads are
+// issued, so the barrier overlaps memory latency.
+__device__ __forceinline__ void block_codebook_lds(float* cb) {
+    if (threadIdx.x < 16) {
+        cb[threadIdx.x] = nf4_code_value(static_cast<int>(threadIdx.x));
     }
-    __builtin_amdgcn_wave_barrier();
 }
 
 }  // namespace kc

@@ -168,7 +168,7 @@ __device__ __forceinline__ void row_epilogue(const Nf4RowsArgs& a, const RowPair
 // stream in, and each task's dot waits only for its own rows.
 template <typename T, RowMode MODE, int TPW>
 __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs a, int64_t ntasks) {
-    __shared__ float cb_all[kRowsThreads / 64][16];
+    __shared__ float cb[16];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t waves_per_block = kRowsThreads / 64;
@@ -220,8 +220,8 @@ __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs 
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    float* cb = cb_all[wave];
-    wave_codebook_lds(cb, lane);
+    block_codebook_lds(cb);
+    __syncthreads();
 
     // RMSNorm of the lane's 32 elements against the whole vector
     float xn[32];
@@ -280,7 +280,7 @@ __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs 
 template <typename T, int NCHUNK, int R>
 __global__ __launch_bounds__(64 * ((NCHUNK + 63) / 64)) void nf4_down_kernel(Nf4DownArgs a) {
     constexpr int W = (NCHUNK + 63) / 64;
-    __shared__ float cb_all[W][16];
+    __shared__ float cb[16];
     __shared__ float red[R][W];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -314,8 +314,8 @@ __global__ __launch_bounds__(64 * ((NCHUNK + 63) / 64)) void nf4_down_kernel(Nf4
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    float* cb = cb_all[wave];
-    wave_codebook_lds(cb, lane);
+    block_codebook_lds(cb);
+    __syncthreads();
     float xv[32];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {

@@ -58,17 +58,16 @@ __device__ __forceinline__ int64_t read_kv_len(const GqaArgs& a) {
     return L < 0 ? 0 : (L > a.capacity ? a.capacity : L);
 }
 
-__device__ __forceinline__ void load_round(const uint16_t* kbase, const uint16_t* vbase, int64_t tk, int nvalid,
-                                           uint4* kr, uint4* vr) {
+// K and V rows of tokens tk .. tk+3 for one lane (dims 8li..8li+7); indices
+// past `last` re-read row `last` (read, never used), so the loads are
+// unconditional and the wave's memory counter stays exact.
+__device__ __forceinline__ void load_rows(const uint16_t* kbase, const uint16_t* vbase, int64_t tk, int64_t last,
+                                          uint4* kr, uint4* vr) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        if (k < nvalid) {
-            kr[k] = *reinterpret_cast<const uint4*>(kbase + (tk + k) * kDim);
-            vr[k] = *reinterpret_cast<const uint4*>(vbase + (tk + k) * kDim);
-        } else {
-            kr[k] = make_uint4(0, 0, 0, 0);
-            vr[k] = make_uint4(0, 0, 0, 0);
-        }
+        const int64_t t = tk + k < last ? tk + k : last;
+        kr[k] = *reinterpret_cast<const uint4*>(kbase + t * kDim);
+        vr[k] = *reinterpret_cast<const uint4*>(vbase + t * kDim);
     }
 }
 
@@ -76,7 +75,7 @@ __device__ __forceinline__ int clamp4(int64_t n) { return static_cast<int>(n < 0
 
 template <typename T>
 __global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a, int merge_mode) {
-    __shared__ float s_x[kGroups][kSlot];
+    __shared__ __attribute__((aligned(16))) float s_x[kGroups][kSlot];
     // group states, head-major so a thread reads one head's 32 groups as
     // 8 contiguous 16-byte loads
     __shared__ __attribute__((aligned(16))) float s_m[kHeadsPerGroup][kGroups];
@@ -106,11 +105,9 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a, int
     for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
         qr[hl] = *reinterpret_cast<const uint4*>(a.q + (g * kHeadsPerGroup + hl) * kDim + 8 * li);
     }
-    uint4 kr[4], vr[4];
-    int spec = 0;
+    uint4 kA[4], vA[4], kB[4], vB[4];
     if (s == 0) {
-        spec = clamp4(a.capacity - 4 * gi);
-        load_round(kbase, vbase, 4 * gi, spec, kr, vr);
+        load_rows(kbase, vbase, 4 * gi, a.capacity - 1, kA, vA);
     }
     const int64_t L = read_kv_len(a);
     const int64_t nsplit = (L + C - 1) / C;
@@ -136,46 +133,56 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a, int
     }
     float* slot = s_x[gi];
 
-    if (s != 0) {
-        load_round(kbase, vbase, t0 + 4 * gi, clamp4(tend - (t0 + 4 * gi)), kr, vr);
-    }
-    for (int64_t base = t0; base < tend; base += kRoundTokens) {
+    // One 128-token round: group gi takes tokens base + 4gi + {0..3}.
+    auto round = [&](const uint4* ck, const uint4* cv_in, int64_t base) {
         const int cur_valid = clamp4(tend - (base + 4 * gi));
-        uint4 ck[4], cv[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            ck[k] = kr[k];
-            cv[k] = vr[k];
-        }
-        const int64_t nbase = base + kRoundTokens;
-        if (nbase < tend) {  // next round's rows load while this one computes
-            load_round(kbase, vbase, nbase + 4 * gi, clamp4(tend - (nbase + 4 * gi)), kr, vr);
-        }
-
-        // scores: every lane of the group gets the sums, lane 0 files them
+        // scores, one token at a time: 8 partial dots per lane, the 16-lane
+        // butterfly (distances 8, 4, 2, 1) stage by stage over the 8 heads,
+        // lane 0 files the scaled sums as two float4
+        float4* out4 = reinterpret_cast<float4*>(slot);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             float kf[8];
             unpack8<T>(ck[k], kf);
+            float d[kHeadsPerGroup];
 #pragma unroll
             for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
-                float d = 0.0f;
+                float t = 0.0f;
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    d = fmaf(q[hl][j], kf[j], d);
+                    t = fmaf(q[hl][j], kf[j], t);
                 }
-                const float sc = group16_sum(d) * a.qk_scale_log2;
-                if (li == 0) {
-                    slot[k * 8 + hl] = sc;
-                }
+                d[hl] = t;
+            }
+#pragma unroll
+            for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
+                d[hl] += row_ror<8>(d[hl]);
+            }
+#pragma unroll
+            for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
+                d[hl] += row_ror<4>(d[hl]);
+            }
+#pragma unroll
+            for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
+                d[hl] += row_ror<2>(d[hl]);
+            }
+#pragma unroll
+            for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
+                d[hl] += row_ror<1>(d[hl]);
+            }
+            if (li == 0) {
+                const float sc = a.qk_scale_log2;
+                out4[2 * k] = make_float4(d[0] * sc, d[1] * sc, d[2] * sc, d[3] * sc);
+                out4[2 * k + 1] = make_float4(d[4] * sc, d[5] * sc, d[6] * sc, d[7] * sc);
             }
         }
         if (cur_valid == 0) {
-            continue;
+            return;  // this group has no token in this round
         }
         __builtin_amdgcn_wave_barrier();
         // lane li < 8: online-softmax step of head li; slot k*8+li becomes
-        // p = exp2(s - m_new), slot 32+li the rescale exp2(m_old - m_new)
+        // p = exp2(s - m_new) (0 for a token past the end), slot 32+li the
+        // rescale exp2(m_old - m_new)
         if (li < kHeadsPerGroup) {
             float sc[4];
             float mt = kNegInf;
@@ -191,11 +198,12 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a, int
             l_own = l_own * corr;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
+                float pk = 0.0f;
                 if (k < cur_valid) {
-                    const float p = exp2_fixed(sc[k] - mnew);
-                    l_own = l_own + p;
-                    slot[k * 8 + li] = p;
+                    pk = exp2_fixed(sc[k] - mnew);
+                    l_own = l_own + pk;
                 }
+                slot[k * 8 + li] = pk;
             }
             slot[32 + li] = corr;
             m_own = mnew;
@@ -209,22 +217,46 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a, int
                 acc[hl][j] = acc[hl][j] * corr;
             }
         }
+        // rows past the end contribute 0 * 0: acc is never -0, so
+        // fmaf(0, 0, acc) == acc and no branch is needed
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            if (k < cur_valid) {
-                float vf[8];
-                unpack8<T>(cv[k], vf);
+            const uint4 raw = k < cur_valid ? cv_in[k] : make_uint4(0, 0, 0, 0);
+            float vf[8];
+            unpack8<T>(raw, vf);
 #pragma unroll
-                for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
-                    const float p = slot[k * 8 + hl];
+            for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
+                const float pk = slot[k * 8 + hl];
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        acc[hl][j] = fmaf(p, vf[j], acc[hl][j]);
-                    }
+                for (int j = 0; j < 8; ++j) {
+                    acc[hl][j] = fmaf(pk, vf[j], acc[hl][j]);
                 }
             }
         }
         __builtin_amdgcn_wave_barrier();
+    };
+
+    // Ping-pong over two register sets: the next round's rows (clamped, so
+    // unconditional) load while the current round computes.
+    const int64_t last = tend - 1;
+    if (s != 0) {
+        load_rows(kbase, vbase, t0 + 4 * gi, last, kA, vA);
+    }
+    for (int64_t base = t0;;) {
+        int64_t nb = base + kRoundTokens;
+        load_rows(kbase, vbase, nb + 4 * gi, last, kB, vB);
+        round(kA, vA, base);
+        if (nb >= tend) {
+            break;
+        }
+        base = nb;
+        nb = base + kRoundTokens;
+        load_rows(kbase, vbase, nb + 4 * gi, last, kA, vA);
+        round(kB, vB, base);
+        if (nb >= tend) {
+            break;
+        }
+        base = nb;
     }
 
     // ---- merge the group states of this block (per head, groups in order;

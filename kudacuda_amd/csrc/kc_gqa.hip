@@ -1,10 +1,21 @@
 // Split-KV grouped-query decode attention for the Qwen2.5-3B shape
 // (16 query heads, 2 KV heads, group 8, head_dim 128).
 //
-// Partial kernel, grid (max_splits, 2): block (s, g) owns tokens
-// [s*C, min(s*C+C, L)) of KV head g and serves all 8 query heads of the
-// group, so every K/V byte is read once.  A block is 8 waves = 32 groups of 16
-// lanes; lane li of a group holds dims [8li, 8li+8) of all 8 query heads.  Per
+// Partial kernel, grid (max_splits, 2): block (s, g) owns one split of the
+// tokens of KV head g and serves all 8 query heads of the group, so every K/V
+// byte is read once.  A block is 8 waves = 32 groups of 16 lanes; lane li of a
+// group holds dims [8li, 8li+8) of all 8 query heads.  Two paths, chosen per
+// launch from kv_len L (uniform over the grid):
+//
+// Flat path (L <= flat_max, at most 16 splits): split s owns tokens
+// [32s, min(32s+32, L)), one per group.  Each group forms its token's 8 head
+// scores (8-dim partial dots and the 16-lane butterfly below), the block takes
+// the per-head max M over the split, weights w_t = exp2(s_t - M), sum
+// l = w_0 + w_1 + ..., and acc[d] = sum_t w_t v_t[d] in token order, with the
+// V rows staged in LDS.  Short caches thus spread over up to 32 CUs instead of
+// running a long per-group chain on 2.
+//
+// Round path (longer L): split s owns tokens [s*C, min(s*C+C, L)).  Per
 // 128-token round, group gi takes tokens base + 4gi + {0..3}: 8 dot products
 // of 8 dims per lane and a 16-lane butterfly (DPP) give every lane of the group
 // all 32 (token, head) scores (log2 domain: pre-multiplied by scale*log2e).
@@ -16,18 +27,23 @@
 // split 0 issues its first rows before kv_len arrives.
 // The 32 group states are merged through LDS (weights exp2(m_g - M) computed
 // once per group and head) into one (max, sum, acc[128]) split partial per
-// head.  Then:
-//   * a single split finishes in place: out = acc*1 / (sum*1), the general
+// head.
+//
+// Either path ends with one (max, sum, acc[128]) partial per split and head.
+// Then, by the number of splits at this L:
+//   * one split finishes in place: out = acc*1 / (sum*1), the general
 //     merge formula with weight exp2(0) = 1 (no ticket, no fences);
 //   * up to kInKernelSplits splits: the partial is written and the last block
 //     of the KV head to finish (device-scope ticket, reset by that block, so
 //     the launch is capture-safe) merges the splits;
 //   * more splits: the partials are merged by gqa_merge_kernel (grid: query
-//     head x 16-dim slice; partials staged through LDS in one pass) launched
-//     right after.
-// Every path sums the splits in index order with the same operations, so the
-// result depends only on (inputs, kv_len, C).  kv_len may come from device
-// memory (graph replay); C comes from the cache length (gqa_chunk_for).
+//     head x 16-dim slice; partials staged through LDS in one pass), which is
+//     launched after the partial kernel whenever the grid allows more than
+//     kInKernelSplits splits and returns at once when L needs fewer.
+// Every merge sums the splits in index order with the same operations, so the
+// result depends only on (inputs, kv_len, C, flat_max).  kv_len may come from
+// device memory (graph replay); C and flat_max come from the cache length
+// (gqa_plan), so a direct call and a graph replay at the same L agree.
 //
 // Math follows the reference's split-KV workspace kernels
 // (kernels/common/qwen2_gqa_workspace.cuh:13-120: per-tile max, sum and
@@ -48,6 +64,8 @@ constexpr int kHeadsPerGroup = 8;
 constexpr int kDim = 128;
 constexpr int kPartialStride = 2 + kDim;
 constexpr int kInKernelSplits = 16;
+constexpr int kFlatTokens = kGroups;        // flat path: one token per group, one round per split
+constexpr int kFlatSplits = kInKernelSplits;
 constexpr int kMergeMaxSplits = 1024;
 constexpr int kMergeDims = 16;              // dims per merge block
 constexpr int kSlot = 40;                   // per-group LDS exchange: 32 scores + 8 rescales
@@ -56,6 +74,11 @@ constexpr float kNegInf = -__builtin_huge_valf();
 __device__ __forceinline__ int64_t read_kv_len(const GqaArgs& a) {
     int64_t L = a.kv_len_device != nullptr ? static_cast<int64_t>(*a.kv_len_device) + a.kv_len_offset : a.kv_len_host;
     return L < 0 ? 0 : (L > a.capacity ? a.capacity : L);
+}
+
+// number of splits that hold tokens at kv_len L (flat or round path)
+__device__ __forceinline__ int64_t split_count(const GqaArgs& a, int64_t L) {
+    return L <= a.flat_max ? (L + kFlatTokens - 1) / kFlatTokens : (L + a.chunk - 1) / a.chunk;
 }
 
 // K and V rows of tokens tk .. tk+3 for one lane (dims 8li..8li+7); indices
@@ -74,7 +97,7 @@ __device__ __forceinline__ void load_rows(const uint16_t* kbase, const uint16_t*
 __device__ __forceinline__ int clamp4(int64_t n) { return static_cast<int>(n < 0 ? 0 : (n > 4 ? 4 : n)); }
 
 template <typename T>
-__global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a, int merge_mode) {
+__global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a) {
     __shared__ __attribute__((aligned(16))) float s_x[kGroups][kSlot];
     // group states, head-major so a thread reads one head's 32 groups as
     // 8 contiguous 16-byte loads
@@ -105,238 +128,334 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a, int
     for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
         qr[hl] = *reinterpret_cast<const uint4*>(a.q + (g * kHeadsPerGroup + hl) * kDim + 8 * li);
     }
+    // flat-path row of this group (token s*32 + gi, bounded by the capacity)
+    uint4 kF = make_uint4(0, 0, 0, 0), vF = make_uint4(0, 0, 0, 0);
+    if (s * kFlatTokens < a.flat_max) {
+        const int64_t t = s * kFlatTokens + gi;
+        const int64_t tc = t < a.capacity ? t : a.capacity - 1;
+        kF = *reinterpret_cast<const uint4*>(kbase + tc * kDim);
+        vF = *reinterpret_cast<const uint4*>(vbase + tc * kDim);
+    }
     uint4 kA[4], vA[4], kB[4], vB[4];
     if (s == 0) {
         load_rows(kbase, vbase, 4 * gi, a.capacity - 1, kA, vA);
     }
     const int64_t L = read_kv_len(a);
-    const int64_t nsplit = (L + C - 1) / C;
+    const int64_t nsplit = split_count(a, L);
     if (s >= nsplit) {
         return;
     }
-    const int64_t tend = (t0 + C < L) ? t0 + C : L;
 
     float q[kHeadsPerGroup][8];
 #pragma unroll
     for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
         unpack8<T>(qr[hl], q[hl]);
     }
-    // softmax state of head li lives in lane li (< 8) of each group
-    float m_own = kNegInf, l_own = 0.0f;
-    float acc[kHeadsPerGroup][8];
-#pragma unroll
-    for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            acc[hl][j] = 0.0f;
-        }
-    }
-    float* slot = s_x[gi];
+    float av_out[2];
 
-    // One 128-token round: group gi takes tokens base + 4gi + {0..3}.
-    auto round = [&](const uint4* ck, const uint4* cv_in, int64_t base) {
-        const int cur_valid = clamp4(tend - (base + 4 * gi));
-        // scores, one token at a time: 8 partial dots per lane, the 16-lane
-        // butterfly (distances 8, 4, 2, 1) stage by stage over the 8 heads,
-        // lane 0 files the scaled sums as two float4
-        float4* out4 = reinterpret_cast<float4*>(slot);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            float kf[8];
-            unpack8<T>(ck[k], kf);
-            float d[kHeadsPerGroup];
-#pragma unroll
-            for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
-                float t = 0.0f;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    t = fmaf(q[hl][j], kf[j], t);
-                }
-                d[hl] = t;
-            }
-#pragma unroll
-            for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
-                d[hl] += row_ror<8>(d[hl]);
-            }
-#pragma unroll
-            for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
-                d[hl] += row_ror<4>(d[hl]);
-            }
-#pragma unroll
-            for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
-                d[hl] += row_ror<2>(d[hl]);
-            }
-#pragma unroll
-            for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
-                d[hl] += row_ror<1>(d[hl]);
-            }
-            if (li == 0) {
-                const float sc = a.qk_scale_log2;
-                out4[2 * k] = make_float4(d[0] * sc, d[1] * sc, d[2] * sc, d[3] * sc);
-                out4[2 * k + 1] = make_float4(d[4] * sc, d[5] * sc, d[6] * sc, d[7] * sc);
-            }
-        }
-        if (cur_valid == 0) {
-            return;  // this group has no token in this round
-        }
-        __builtin_amdgcn_wave_barrier();
-        // lane li < 8: online-softmax step of head li; slot k*8+li becomes
-        // p = exp2(s - m_new) (0 for a token past the end), slot 32+li the
-        // rescale exp2(m_old - m_new)
-        if (li < kHeadsPerGroup) {
-            float sc[4];
-            float mt = kNegInf;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                sc[k] = slot[k * 8 + li];
-                if (k < cur_valid) {
-                    mt = fmaxf(mt, sc[k]);
-                }
-            }
-            const float mnew = fmaxf(m_own, mt);
-            const float corr = exp2_fixed(m_own - mnew);
-            l_own = l_own * corr;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                float pk = 0.0f;
-                if (k < cur_valid) {
-                    pk = exp2_fixed(sc[k] - mnew);
-                    l_own = l_own + pk;
-                }
-                slot[k * 8 + li] = pk;
-            }
-            slot[32 + li] = corr;
-            m_own = mnew;
-        }
-        __builtin_amdgcn_wave_barrier();
+    if (L <= a.flat_max) {
+        // ---- flat path: group gi scores token s*32 + gi for the 8 heads
+        // (same dot and butterfly as a round), then one block-wide softmax
+        // per head over the split's tokens and the weighted V sum from LDS.
+        float (*s_vf)[kDim] = reinterpret_cast<float (*)[kDim]>(&s_acc[0][0][0]);
+        const int64_t f0 = s * kFlatTokens;
+        const int nvalid = static_cast<int>(f0 + kFlatTokens < L ? kFlatTokens : L - f0);
+        float kf[8], vf[8];
+        unpack8<T>(kF, kf);
+        unpack8<T>(vF, vf);
+        float dots[kHeadsPerGroup];
 #pragma unroll
         for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
-            const float corr = slot[32 + hl];
+            float t = 0.0f;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                acc[hl][j] = acc[hl][j] * corr;
+                t = fmaf(q[hl][j], kf[j], t);
+            }
+            dots[hl] = t;
+        }
+#pragma unroll
+        for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
+            dots[hl] += row_ror<8>(dots[hl]);
+        }
+#pragma unroll
+        for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
+            dots[hl] += row_ror<4>(dots[hl]);
+        }
+#pragma unroll
+        for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
+            dots[hl] += row_ror<2>(dots[hl]);
+        }
+#pragma unroll
+        for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
+            dots[hl] += row_ror<1>(dots[hl]);
+        }
+        float mine = dots[0];
+#pragma unroll
+        for (int hl = 1; hl < kHeadsPerGroup; ++hl) {
+            mine = li == hl ? dots[hl] : mine;
+        }
+        if (li < kHeadsPerGroup) {
+            s_m[li][gi] = mine * a.qk_scale_log2;  // score of (token gi, head li)
+        }
+        float4* vrow = reinterpret_cast<float4*>(&s_vf[gi][8 * li]);
+        vrow[0] = make_float4(vf[0], vf[1], vf[2], vf[3]);
+        vrow[1] = make_float4(vf[4], vf[5], vf[6], vf[7]);
+        __syncthreads();
+        if (threadIdx.x < kGroups * kHeadsPerGroup) {
+            const int hl = threadIdx.x / kGroups;
+            const int gg = threadIdx.x % kGroups;
+            float sv[kGroups];
+#pragma unroll
+            for (int x = 0; x < kGroups; ++x) {
+                sv[x] = s_m[hl][x];
+            }
+            float M = kNegInf;
+#pragma unroll
+            for (int x = 0; x < kGroups; ++x) {
+                M = x < nvalid ? fmaxf(M, sv[x]) : M;
+            }
+            s_w[hl][gg] = gg < nvalid ? exp2_fixed(s_m[hl][gg] - M) : 0.0f;
+            if (gg == 0) {
+                s_M[hl] = M;
             }
         }
-        // rows past the end contribute 0 * 0: acc is never -0, so
-        // fmaf(0, 0, acc) == acc and no branch is needed
+        __syncthreads();
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint4 raw = k < cur_valid ? cv_in[k] : make_uint4(0, 0, 0, 0);
-            float vf[8];
-            unpack8<T>(raw, vf);
+        for (int half = 0; half < 2; ++half) {
+            const int hl = half * 4 + threadIdx.x / kDim;
+            const int dd = threadIdx.x % kDim;
+            float acc_f = 0.0f;
+            float lsum = 0.0f;
+#pragma unroll 8
+            for (int x = 0; x < nvalid; ++x) {
+                const float w = s_w[hl][x];
+                acc_f = fmaf(w, s_vf[x][dd], acc_f);
+                lsum = lsum + w;
+            }
+            av_out[half] = acc_f;
+            if (dd == 0) {
+                s_L[hl] = lsum;
+            }
+        }
+        __syncthreads();
+    } else {
+        const int64_t tend = (t0 + C < L) ? t0 + C : L;
+        // softmax state of head li lives in lane li (< 8) of each group
+        float m_own = kNegInf, l_own = 0.0f;
+        float acc[kHeadsPerGroup][8];
 #pragma unroll
-            for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
-                const float pk = slot[k * 8 + hl];
+        for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    acc[hl][j] = fmaf(pk, vf[j], acc[hl][j]);
+            for (int j = 0; j < 8; ++j) {
+                acc[hl][j] = 0.0f;
+            }
+        }
+        float* slot = s_x[gi];
+
+        // One 128-token round: group gi takes tokens base + 4gi + {0..3}.
+        auto round = [&](const uint4* ck, const uint4* cv_in, int64_t base) {
+            const int cur_valid = clamp4(tend - (base + 4 * gi));
+            // scores, one token at a time: 8 partial dots per lane, the 16-lane
+            // butterfly (distances 8, 4, 2, 1) stage by stage over the 8 heads,
+            // lane 0 files the scaled sums as two float4
+            float4* out4 = reinterpret_cast<float4*>(slot);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                float kf[8];
+                unpack8<T>(ck[k], kf);
+                float d[kHeadsPerGroup];
+#pragma unroll
+                for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
+                    float t = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        t = fmaf(q[hl][j], kf[j], t);
+                    }
+                    d[hl] = t;
+                }
+#pragma unroll
+                for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
+                    d[hl] += row_ror<8>(d[hl]);
+                }
+#pragma unroll
+                for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
+                    d[hl] += row_ror<4>(d[hl]);
+                }
+#pragma unroll
+                for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
+                    d[hl] += row_ror<2>(d[hl]);
+                }
+#pragma unroll
+                for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
+                    d[hl] += row_ror<1>(d[hl]);
+                }
+                if (li == 0) {
+                    const float sc = a.qk_scale_log2;
+                    out4[2 * k] = make_float4(d[0] * sc, d[1] * sc, d[2] * sc, d[3] * sc);
+                    out4[2 * k + 1] = make_float4(d[4] * sc, d[5] * sc, d[6] * sc, d[7] * sc);
                 }
             }
-        }
-        __builtin_amdgcn_wave_barrier();
-    };
+            if (cur_valid == 0) {
+                return;  // this group has no token in this round
+            }
+            __builtin_amdgcn_wave_barrier();
+            // lane li < 8: online-softmax step of head li; slot k*8+li becomes
+            // p = exp2(s - m_new) (0 for a token past the end), slot 32+li the
+            // rescale exp2(m_old - m_new)
+            if (li < kHeadsPerGroup) {
+                float sc[4];
+                float mt = kNegInf;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    sc[k] = slot[k * 8 + li];
+                    if (k < cur_valid) {
+                        mt = fmaxf(mt, sc[k]);
+                    }
+                }
+                const float mnew = fmaxf(m_own, mt);
+                const float corr = exp2_fixed(m_own - mnew);
+                l_own = l_own * corr;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    float pk = 0.0f;
+                    if (k < cur_valid) {
+                        pk = exp2_fixed(sc[k] - mnew);
+                        l_own = l_own + pk;
+                    }
+                    slot[k * 8 + li] = pk;
+                }
+                slot[32 + li] = corr;
+                m_own = mnew;
+            }
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
+                const float corr = slot[32 + hl];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    acc[hl][j] = acc[hl][j] * corr;
+                }
+            }
+            // rows past the end contribute 0 * 0: acc is never -0, so
+            // fmaf(0, 0, acc) == acc and no branch is needed
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint4 raw = k < cur_valid ? cv_in[k] : make_uint4(0, 0, 0, 0);
+                float vf[8];
+                unpack8<T>(raw, vf);
+#pragma unroll
+                for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
+                    const float pk = slot[k * 8 + hl];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        acc[hl][j] = fmaf(pk, vf[j], acc[hl][j]);
+                    }
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+        };
 
-    // Ping-pong over two register sets: the next round's rows (clamped, so
-    // unconditional) load while the current round computes.
-    const int64_t last = tend - 1;
-    if (s != 0) {
-        load_rows(kbase, vbase, t0 + 4 * gi, last, kA, vA);
-    }
-    for (int64_t base = t0;;) {
-        int64_t nb = base + kRoundTokens;
-        load_rows(kbase, vbase, nb + 4 * gi, last, kB, vB);
-        round(kA, vA, base);
-        if (nb >= tend) {
-            break;
+        // Ping-pong over two register sets: the next round's rows (clamped, so
+        // unconditional) load while the current round computes.
+        const int64_t last = tend - 1;
+        if (s != 0) {
+            load_rows(kbase, vbase, t0 + 4 * gi, last, kA, vA);
         }
-        base = nb;
-        nb = base + kRoundTokens;
-        load_rows(kbase, vbase, nb + 4 * gi, last, kA, vA);
-        round(kB, vB, base);
-        if (nb >= tend) {
-            break;
+        for (int64_t base = t0;;) {
+            int64_t nb = base + kRoundTokens;
+            load_rows(kbase, vbase, nb + 4 * gi, last, kB, vB);
+            round(kA, vA, base);
+            if (nb >= tend) {
+                break;
+            }
+            base = nb;
+            nb = base + kRoundTokens;
+            load_rows(kbase, vbase, nb + 4 * gi, last, kA, vA);
+            round(kB, vB, base);
+            if (nb >= tend) {
+                break;
+            }
+            base = nb;
         }
-        base = nb;
-    }
 
-    // ---- merge the group states of this block (per head, groups in order;
-    // a group that saw no token is skipped)
-    if (li < kHeadsPerGroup) {
-        s_m[li][gi] = m_own;
-        s_l[li][gi] = l_own;
-    }
-    __syncthreads();
-    if (threadIdx.x < kGroups * kHeadsPerGroup) {
-        const int hl = threadIdx.x / kGroups;
-        const int gg = threadIdx.x % kGroups;
-        float mv[kGroups];
-#pragma unroll
-        for (int x = 0; x < kGroups; ++x) {
-            mv[x] = s_m[hl][x];
+        // ---- merge the group states of this block (per head, groups in order;
+        // a group that saw no token is skipped)
+        if (li < kHeadsPerGroup) {
+            s_m[li][gi] = m_own;
+            s_l[li][gi] = l_own;
         }
-        float M = kNegInf;
-#pragma unroll
-        for (int x = 0; x < kGroups; ++x) {
-            M = fmaxf(M, mv[x]);
-        }
-        const float mg = s_m[hl][gg];
-        s_w[hl][gg] = mg == kNegInf ? 0.0f : exp2_fixed(mg - M);
-        if (gg == 0) {
-            s_M[hl] = M;
-        }
-    }
-    __syncthreads();
-    if (threadIdx.x < kHeadsPerGroup) {
-        const int hl = threadIdx.x;
-        float mv[kGroups], lv[kGroups], wv[kGroups];
-#pragma unroll
-        for (int x = 0; x < kGroups; ++x) {
-            mv[x] = s_m[hl][x];
-            lv[x] = s_l[hl][x];
-            wv[x] = s_w[hl][x];
-        }
-        float lsum = 0.0f;
-#pragma unroll
-        for (int x = 0; x < kGroups; ++x) {
-            const float t = fmaf(lv[x], wv[x], lsum);
-            lsum = mv[x] != kNegInf ? t : lsum;
-        }
-        s_L[hl] = lsum;
-    }
-
-    // merged acc of the block: thread t owns (hl = half*4 + t/128, d = t%128)
-    float av_out[2];
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
         __syncthreads();
+        if (threadIdx.x < kGroups * kHeadsPerGroup) {
+            const int hl = threadIdx.x / kGroups;
+            const int gg = threadIdx.x % kGroups;
+            float mv[kGroups];
 #pragma unroll
-        for (int hh = 0; hh < kHeadsPerGroup / 2; ++hh) {
+            for (int x = 0; x < kGroups; ++x) {
+                mv[x] = s_m[hl][x];
+            }
+            float M = kNegInf;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                s_acc[gi][hh][8 * li + j] = acc[half * 4 + hh][j];
+            for (int x = 0; x < kGroups; ++x) {
+                M = fmaxf(M, mv[x]);
+            }
+            const float mg = s_m[hl][gg];
+            s_w[hl][gg] = mg == kNegInf ? 0.0f : exp2_fixed(mg - M);
+            if (gg == 0) {
+                s_M[hl] = M;
             }
         }
         __syncthreads();
-        const int hh = threadIdx.x / kDim;
-        const int d = threadIdx.x % kDim;
-        const int hl = half * 4 + hh;
-        float mv[kGroups], wv[kGroups], xv[kGroups];
+        if (threadIdx.x < kHeadsPerGroup) {
+            const int hl = threadIdx.x;
+            float mv[kGroups], lv[kGroups], wv[kGroups];
 #pragma unroll
-        for (int x = 0; x < kGroups; ++x) {
-            mv[x] = s_m[hl][x];
-            wv[x] = s_w[hl][x];
-            xv[x] = s_acc[x][hh][d];
-        }
-        float av = 0.0f;
+            for (int x = 0; x < kGroups; ++x) {
+                mv[x] = s_m[hl][x];
+                lv[x] = s_l[hl][x];
+                wv[x] = s_w[hl][x];
+            }
+            float lsum = 0.0f;
 #pragma unroll
-        for (int x = 0; x < kGroups; ++x) {
-            const float t = fmaf(xv[x], wv[x], av);
-            av = mv[x] != kNegInf ? t : av;
+            for (int x = 0; x < kGroups; ++x) {
+                const float t = fmaf(lv[x], wv[x], lsum);
+                lsum = mv[x] != kNegInf ? t : lsum;
+            }
+            s_L[hl] = lsum;
         }
-        av_out[half] = av;
+
+        // merged acc of the block: thread t owns (hl = half*4 + t/128, d = t%128)
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            __syncthreads();
+#pragma unroll
+            for (int hh = 0; hh < kHeadsPerGroup / 2; ++hh) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    s_acc[gi][hh][8 * li + j] = acc[half * 4 + hh][j];
+                }
+            }
+            __syncthreads();
+            const int hh = threadIdx.x / kDim;
+            const int d = threadIdx.x % kDim;
+            const int hl = half * 4 + hh;
+            float mv[kGroups], wv[kGroups], xv[kGroups];
+#pragma unroll
+            for (int x = 0; x < kGroups; ++x) {
+                mv[x] = s_m[hl][x];
+                wv[x] = s_w[hl][x];
+                xv[x] = s_acc[x][hh][d];
+            }
+            float av = 0.0f;
+#pragma unroll
+            for (int x = 0; x < kGroups; ++x) {
+                const float t = fmaf(xv[x], wv[x], av);
+                av = mv[x] != kNegInf ? t : av;
+            }
+            av_out[half] = av;
+        }
     }
 
-    if (nsplit == 1 && merge_mode != 2) {
+    if (nsplit == 1) {
         // single split: the general merge with weight exp2(M - M) = 1
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
@@ -362,7 +481,7 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a, int
             store_agent(dst + 1, s_L[hl]);
         }
     }
-    if (merge_mode == 2) {
+    if (nsplit > kInKernelSplits) {
         return;  // gqa_merge_kernel follows
     }
 
@@ -433,9 +552,9 @@ __global__ __launch_bounds__(256) void gqa_merge_kernel(GqaArgs a) {
     const int h = blockIdx.x;
     const int d0 = blockIdx.y * kMergeDims;
     const int64_t L = read_kv_len(a);
-    const int nsplit = static_cast<int>((L + a.chunk - 1) / a.chunk);
-    if (nsplit < 1) {
-        return;
+    const int nsplit = static_cast<int>(split_count(a, L));
+    if (nsplit <= kInKernelSplits) {
+        return;  // merged by the partial kernel
     }
     const float* src = a.partials + static_cast<int64_t>(h) * a.max_splits * kPartialStride;
     float mloc = kNegInf;
@@ -509,19 +628,40 @@ __global__ __launch_bounds__(256) void gqa_merge_kernel(GqaArgs a) {
 
 int64_t gqa_chunk_for(int64_t) { return 2 * kRoundTokens; }
 
+GqaPlan gqa_plan(int64_t capacity, int64_t split_limit) {
+    GqaPlan p;
+    p.chunk = gqa_chunk_for(capacity);
+    int64_t flat_splits = kFlatSplits;
+    if (split_limit > 0 && split_limit < flat_splits) {
+        flat_splits = split_limit;
+    }
+    p.flat_max = flat_splits * kFlatTokens;
+    if (p.flat_max > capacity) {
+        p.flat_max = capacity;
+    }
+    const int64_t round_splits = (capacity + p.chunk - 1) / p.chunk;
+    const int64_t flat = (p.flat_max + kFlatTokens - 1) / kFlatTokens;
+    p.max_splits = round_splits > flat ? round_splits : flat;
+    return p;
+}
+
 hipError_t launch_gqa_decode(Act act, const GqaArgs& a, hipStream_t stream) {
-    if (a.max_splits <= 0 || a.max_splits > kMergeMaxSplits || a.chunk <= 0 || a.chunk % kRoundTokens != 0) {
+    // the grid must cover every split either path can produce
+    const int64_t flat_splits = (a.flat_max + kFlatTokens - 1) / kFlatTokens;
+    const int64_t round_splits = (a.capacity + a.chunk - 1) / a.chunk;
+    if (a.max_splits <= 0 || a.max_splits > kMergeMaxSplits || a.chunk <= 0 || a.chunk % kRoundTokens != 0 ||
+        a.flat_max < 0 || flat_splits > kFlatSplits || a.capacity <= 0 || round_splits > a.max_splits ||
+        flat_splits > a.max_splits) {
         return hipErrorInvalidValue;
     }
-    const int merge_mode = a.max_splits <= kInKernelSplits ? 1 : 2;
     const dim3 grid(static_cast<unsigned>(a.max_splits), 2);
     if (act == Act::kBf16) {
-        hipLaunchKernelGGL(gqa_partial_kernel<Bf16>, grid, dim3(kGqaThreads), 0, stream, a, merge_mode);
+        hipLaunchKernelGGL(gqa_partial_kernel<Bf16>, grid, dim3(kGqaThreads), 0, stream, a);
     } else {
-        hipLaunchKernelGGL(gqa_partial_kernel<F16>, grid, dim3(kGqaThreads), 0, stream, a, merge_mode);
+        hipLaunchKernelGGL(gqa_partial_kernel<F16>, grid, dim3(kGqaThreads), 0, stream, a);
     }
     hipError_t status = hipGetLastError();
-    if (status != hipSuccess || merge_mode == 1) {
+    if (status != hipSuccess || a.max_splits <= kInKernelSplits) {
         return status;
     }
     const dim3 mgrid(16, kDim / kMergeDims);

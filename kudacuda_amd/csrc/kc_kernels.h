@@ -82,11 +82,20 @@ struct GqaArgs {
     int64_t kv_len_host = 0;
     int64_t capacity = 0;          // row stride of the cache
     int64_t max_splits = 0;        // grid size per KV head
-    int64_t chunk = 64;
+    int64_t chunk = 64;            // tokens per split on the round path
+    int64_t flat_max = 0;          // kv_len <= flat_max takes the flat path (kGqaFlatTokens per split)
     float qk_scale_log2 = 0.0f;    // scale * log2(e)
 };
 hipError_t launch_gqa_decode(Act act, const GqaArgs& args, hipStream_t stream);
-int64_t gqa_chunk_for(int64_t tokens);  // chunk rule shared with the host oracle
+// Split plan for a cache of `capacity` rows; split_limit > 0 caps the number
+// of splits (a caller-sized workspace).  Rule shared with the host oracle.
+struct GqaPlan {
+    int64_t chunk = 0;
+    int64_t flat_max = 0;
+    int64_t max_splits = 0;
+};
+GqaPlan gqa_plan(int64_t capacity, int64_t split_limit);
+int64_t gqa_chunk_for(int64_t tokens);
 
 // ------------------------------------------------------------- lm_head/argmax
 struct LmHeadArgs {

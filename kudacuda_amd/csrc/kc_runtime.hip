@@ -89,12 +89,16 @@ int finish(Handle* h, const char* operation, hipError_t status) {
     return 0;
 }
 
-int64_t gqa_splits(int64_t tokens) {
-    const int64_t chunk = gqa_chunk_for(tokens);
-    return (tokens + chunk - 1) / chunk;
+// split plan of a cache of `capacity` rows into the launch arguments
+void set_gqa_plan(GqaArgs& a, int64_t capacity, int64_t split_limit) {
+    const GqaPlan p = gqa_plan(capacity, split_limit);
+    a.capacity = capacity;
+    a.chunk = p.chunk;
+    a.flat_max = p.flat_max;
+    a.max_splits = p.max_splits;
 }
 
-int64_t gqa_workspace(int64_t tokens) { return 16 * gqa_splits(tokens) * 130; }
+int64_t gqa_workspace(int64_t tokens) { return 16 * gqa_plan(tokens, 0).max_splits * 130; }
 
 const char* const kGfx950Tactics[] = {
     "qwen2_gqa_decode_gfx950_fp16",
@@ -239,9 +243,7 @@ int gqa_direct(void* raw, const char* symbol, Act act, uint64_t q, uint64_t k, u
     a.partials = h->gqa_partials;
     a.counters = h->counters;
     a.kv_len_host = kv_len;
-    a.capacity = kv_len;
-    a.chunk = gqa_chunk_for(kv_len);
-    a.max_splits = gqa_splits(kv_len);
+    set_gqa_plan(a, kv_len, 0);
     a.qk_scale_log2 = s.scale * kLog2e;
     return finish(h, symbol, launch_gqa_decode(act, a, as_stream(stream)));
 }
@@ -268,9 +270,7 @@ int gqa_graph(void* raw, const char* symbol, Act act, uint64_t q, uint64_t k, ui
     a.partials = h->gqa_partials;
     a.counters = h->counters;
     a.kv_len_device = ptr<const int32_t>(kv_len_device);
-    a.capacity = kv_capacity;
-    a.chunk = gqa_chunk_for(kv_capacity);
-    a.max_splits = gqa_splits(kv_capacity);
+    set_gqa_plan(a, kv_capacity, 0);
     a.qk_scale_log2 = s.scale * kLog2e;
     return finish(h, symbol, launch_gqa_decode(act, a, as_stream(stream)));
 }
@@ -342,9 +342,7 @@ hipError_t model_op(const Model& m, int op, int64_t layer, bool bookkeeping, hip
             a.counters = ptr<uint32_t>(G[KUDACUDA_QWEN2_ATTN_COUNTERS]);
             a.kv_len_device = ptr<const int32_t>(G[KUDACUDA_QWEN2_CONTROL]);
             a.kv_len_offset = 1;
-            a.capacity = m.capacity;
-            a.chunk = gqa_chunk_for(m.capacity);
-            a.max_splits = gqa_splits(m.capacity);
+            set_gqa_plan(a, m.capacity, 0);
             a.qk_scale_log2 = static_cast<float>(1.0 / std::sqrt(128.0)) * kLog2e;
             return launch_gqa_decode(Act::kBf16, a, stream);
         }
@@ -823,9 +821,8 @@ int kudacuda_qwen2_gqa_decode_workspace_v3(void* raw, uint64_t query, uint64_t k
     a.partials = ptr<float>(workspace);
     a.counters = h->counters;
     a.kv_len_device = ptr<const int32_t>(kv_len_device);
-    a.capacity = kv_capacity;
-    a.chunk = kc::gqa_chunk_for(kv_capacity);
-    a.max_splits = (kv_capacity + a.chunk - 1) / a.chunk;
+    // the caller's workspace holds 16 x 8 x 130 floats (reference contract)
+    kc::set_gqa_plan(a, kv_capacity, 8);
     a.qk_scale_log2 = scale * kc::kLog2e;
     return finish(h, symbol, kc::launch_gqa_decode(Act::kF16, a, as_stream(stream)));
 }

@@ -370,15 +370,50 @@ KCO_API void kco_down11008(int act, const uint16_t* x, const uint8_t* w, const f
 #define GQA_GROUPS 32
 #define GQA_ROUND (4 * GQA_GROUPS)
 
-/* tokens per split for a cache of `tokens` rows (the kernels' rule) */
+/* Flat path: kv_len <= flat_max, GQA_GROUPS tokens per split (one per group),
+ * at most GQA_FLAT_SPLITS splits. */
+#define GQA_FLAT_SPLITS 16
+
+/* tokens per split on the round path for a cache of `tokens` rows */
 KCO_API int64_t kco_gqa_chunk_for(int64_t tokens) { (void)tokens; return 2 * GQA_ROUND; }
 
-/* q [16,128], caches [2, capacity, 128], kv_len L, chunk C (multiple of GQA_ROUND). */
+/* The kernels' split plan for a cache of `capacity` rows (split_limit > 0 caps
+ * the splits of the flat path): out = {chunk, flat_max, max_splits}. */
+KCO_API void kco_gqa_plan(int64_t capacity, int64_t split_limit, int64_t* plan) {
+    const int64_t chunk = kco_gqa_chunk_for(capacity);
+    int64_t flat_splits = GQA_FLAT_SPLITS;
+    if (split_limit > 0 && split_limit < flat_splits) flat_splits = split_limit;
+    int64_t flat_max = flat_splits * GQA_GROUPS;
+    if (flat_max > capacity) flat_max = capacity;
+    const int64_t round_splits = (capacity + chunk - 1) / chunk;
+    const int64_t flat = (flat_max + GQA_GROUPS - 1) / GQA_GROUPS;
+    plan[0] = chunk;
+    plan[1] = flat_max;
+    plan[2] = round_splits > flat ? round_splits : flat;
+}
+
+/* 16-lane partial dots of one K row with the 8 query heads of its group,
+ * reduced by the DPP butterfly and scaled into the log2 domain. */
+static void gqa_scores(int act, const float qf[8][128], const uint16_t* krow, float qk_scale_log2, float* s8) {
+    for (int hl = 0; hl < 8; ++hl) {
+        float lanes[16];
+        for (int li = 0; li < 16; ++li) {
+            float dsum = 0.0f;
+            for (int j = 0; j < 8; ++j) dsum = fmaf(qf[hl][8 * li + j], act_load(act, krow[8 * li + j]), dsum);
+            lanes[li] = dsum;
+        }
+        s8[hl] = butterfly(lanes, 16) * qk_scale_log2;
+    }
+}
+
+/* q [16,128], caches [2, capacity, 128], kv_len L, round-path chunk C
+ * (multiple of GQA_ROUND), flat path for L <= flat_max. */
 KCO_API void kco_gqa(int act, const uint16_t* q, const uint16_t* kc, const uint16_t* vc, int64_t capacity,
-                     int64_t L, int64_t C, float qk_scale_log2, uint16_t* out) {
+                     int64_t L, int64_t C, int64_t flat_max, float qk_scale_log2, uint16_t* out) {
     if (L > capacity) L = capacity;
     if (L < 1) return;
-    const int64_t nsplit = (L + C - 1) / C;
+    const int flat = L <= flat_max;
+    const int64_t nsplit = flat ? (L + GQA_GROUPS - 1) / GQA_GROUPS : (L + C - 1) / C;
     float* part = (float*)malloc(sizeof(float) * 16 * (size_t)nsplit * 130);
 #pragma omp parallel for collapse(2) schedule(static)
     for (int g = 0; g < 2; ++g) {
@@ -386,6 +421,36 @@ KCO_API void kco_gqa(int act, const uint16_t* q, const uint16_t* kc, const uint1
             float qf[8][128];
             for (int hl = 0; hl < 8; ++hl)
                 for (int d = 0; d < 128; ++d) qf[hl][d] = act_load(act, q[(8 * g + hl) * 128 + d]);
+            if (flat) {
+                /* one token per group; per head: M = max, w_t = exp2(s_t - M),
+                 * l = sum of w_t and acc = sum of w_t v_t, both in token order */
+                const int64_t f0 = s * GQA_GROUPS;
+                const int nvalid = (int)(f0 + GQA_GROUPS < L ? GQA_GROUPS : L - f0);
+                float sc[GQA_GROUPS][8];
+                for (int t = 0; t < nvalid; ++t)
+                    gqa_scores(act, (const float(*)[128])qf, kc + ((int64_t)g * capacity + f0 + t) * 128,
+                               qk_scale_log2, sc[t]);
+                for (int hl = 0; hl < 8; ++hl) {
+                    float M = -INFINITY;
+                    for (int t = 0; t < nvalid; ++t) M = fmaxf(M, sc[t][hl]);
+                    float w[GQA_GROUPS];
+                    float lsum = 0.0f;
+                    for (int t = 0; t < nvalid; ++t) {
+                        w[t] = exp2_fixed(sc[t][hl] - M);
+                        lsum = lsum + w[t];
+                    }
+                    float* dst = part + ((int64_t)(8 * g + hl) * nsplit + s) * 130;
+                    for (int d = 0; d < 128; ++d) {
+                        float acc = 0.0f;
+                        for (int t = 0; t < nvalid; ++t)
+                            acc = fmaf(w[t], act_load(act, vc[((int64_t)g * capacity + f0 + t) * 128 + d]), acc);
+                        dst[2 + d] = acc;
+                    }
+                    dst[0] = M;
+                    dst[1] = lsum;
+                }
+                continue;
+            }
             float gm[GQA_GROUPS][8], gl[GQA_GROUPS][8];
             static __thread float gacc[GQA_GROUPS][8][128];
             for (int gi = 0; gi < GQA_GROUPS; ++gi)
@@ -403,19 +468,9 @@ KCO_API void kco_gqa(int act, const uint16_t* q, const uint16_t* kc, const uint1
                     nvalid = nvalid < 0 ? 0 : (nvalid > 4 ? 4 : nvalid);
                     if (nvalid == 0) continue;
                     float s2[4][8];
-                    for (int k = 0; k < nvalid; ++k) {
-                        const uint16_t* krow = kc + ((int64_t)g * capacity + tk + k) * 128;
-                        for (int hl = 0; hl < 8; ++hl) {
-                            float lanes[16];
-                            for (int li = 0; li < 16; ++li) {
-                                float dsum = 0.0f;
-                                for (int j = 0; j < 8; ++j)
-                                    dsum = fmaf(qf[hl][8 * li + j], act_load(act, krow[8 * li + j]), dsum);
-                                lanes[li] = dsum;
-                            }
-                            s2[k][hl] = butterfly(lanes, 16) * qk_scale_log2;
-                        }
-                    }
+                    for (int k = 0; k < nvalid; ++k)
+                        gqa_scores(act, (const float(*)[128])qf, kc + ((int64_t)g * capacity + tk + k) * 128,
+                                   qk_scale_log2, s2[k]);
                     for (int hl = 0; hl < 8; ++hl) {
                         float mt = -INFINITY;
                         for (int k = 0; k < nvalid; ++k) mt = fmaxf(mt, s2[k][hl]);
@@ -562,7 +617,8 @@ KCO_API void kco_qwen2_step(int64_t num_layers, int64_t vocab, int64_t capacity,
     int64_t L = (int64_t)control[0] + 1;
     if (L > capacity) L = capacity;
     const float qk_scale_log2 = (float)(1.0 / sqrt(128.0)) * kLog2e;
-    const int64_t chunk = kco_gqa_chunk_for(capacity);
+    int64_t plan[3];
+    kco_gqa_plan(capacity, 0, plan);
     for (int64_t layer = 0; layer < num_layers; ++layer) {
         const uint64_t* Lp = layer_ptrs + layer * L_FIELDS;
         kco_qkv_rope_cache(hidden, P(const uint16_t*, Lp[L_INPUT_NORM]), eps, P(const uint8_t*, Lp[L_Q_PACKED]),
@@ -573,7 +629,7 @@ KCO_API void kco_qwen2_step(int64_t num_layers, int64_t vocab, int64_t capacity,
                            P(const float*, G[M_ROPE_COS]), P(const float*, G[M_ROPE_SIN]), pos, capacity, query,
                            P(uint16_t*, Lp[L_KEY_CACHE]), P(uint16_t*, Lp[L_VALUE_CACHE]));
         kco_gqa(0, query, P(const uint16_t*, Lp[L_KEY_CACHE]), P(const uint16_t*, Lp[L_VALUE_CACHE]), capacity, L,
-                chunk, qk_scale_log2, attn);
+                plan[0], plan[1], qk_scale_log2, attn);
         kco_nf4_gemv2048(0, attn, P(const uint8_t*, Lp[L_O_PACKED]), P(const float*, Lp[L_O_ABSMAX]), NULL, hidden,
                          2048, hidden);
         kco_swiglu(0, hidden, P(const uint16_t*, Lp[L_POST_NORM]), eps, P(const uint8_t*, Lp[L_GATE_PACKED]),

@@ -193,7 +193,8 @@ def test_mlp_config3(torch_gpu, native, stream, with_norm, with_residual):
     _close(host(out), y)
 
 
-KV_LENS = [1, 7, 37, 128, 512, 585, 1024, 2048, 8192, 32768]
+# flat path up to 512 (edges 32/33, 511/512), round path beyond (513 ...)
+KV_LENS = [1, 7, 32, 33, 37, 128, 511, 512, 513, 585, 1024, 2048, 8192, 32768]
 
 
 @pytest.mark.parametrize("kv_len", KV_LENS)
@@ -215,7 +216,8 @@ def test_gqa_decode_bf16_config4(torch_gpu, native, stream, kv_len):
         assert np.array_equal(got.reshape(16, 128), np.repeat(v.reshape(2, 128), 8, axis=0))
 
 
-@pytest.mark.parametrize("kv_len,capacity", [(1, 512), (100, 512), (512, 512), (585, 2048), (2048, 2048)])
+@pytest.mark.parametrize("kv_len,capacity", [(1, 512), (100, 512), (512, 512), (33, 2048), (513, 2048), (585, 2048),
+                                             (2048, 2048), (200, 32768), (8000, 32768)])
 def test_gqa_graph_reads_device_kv_len(torch_gpu, native, stream, kv_len, capacity):
     torch = torch_gpu
     q, k, v = synthetic.gqa_inputs(SEED, kv_len, capacity)
@@ -256,7 +258,9 @@ def test_gqa_workspace_v3(torch_gpu, native, stream):
     capacity = 512
     scale = synthetic.default_scale()
     ws = empty(torch, 16 * 8 * 130, "f32")
-    for kv_len in (1, 7, 64, 128, 512):  # reference tests/qwen2_gqa_workspace_smoke.cu:29-49
+    # reference tests/qwen2_gqa_workspace_smoke.cu:29-49, plus the edge of the
+    # flat path under this 8-split workspace (256 flat, 257 round)
+    for kv_len in (1, 7, 64, 128, 256, 257, 512):
         q, k, v = synthetic.gqa_inputs(SEED + kv_len, kv_len, capacity)
         q16 = O.f32_to_f16(O.bf16_to_f32(q))
         k16 = O.f32_to_f16(O.bf16_to_f32(k)).reshape(2, capacity, 128)
@@ -267,7 +271,7 @@ def test_gqa_workspace_v3(torch_gpu, native, stream):
         native.call("kudacuda_qwen2_gqa_decode_workspace_v3", p(d_q), p(d_k), p(d_v), p(out), p(ws), p(d_len), 1, 1,
                     capacity, 16, 2, 128, scale, stream.cuda_stream)
         stream.synchronize()
-        assert np.array_equal(host(out), O.gqa(q16, k16, v16, kv_len, chunk=O.gqa_chunk_for(capacity), dtype="f16"))
+        assert np.array_equal(host(out), O.gqa(q16, k16, v16, kv_len, split_limit=8, dtype="f16"))
 
 
 @pytest.mark.parametrize("vocab,with_norm", [(151936, True), (1000, False), (1, True)])

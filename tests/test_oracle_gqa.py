@@ -87,3 +87,68 @@ def test_planted_wrong_group_mapping_fails():
     got = O.f16_to_f32(O.gqa(q, k[::-1].copy(), v[::-1].copy(), 37, dtype="f16"))
     want = gqa_f64(O.f16_to_f32(q), O.f16_to_f32(k), O.f16_to_f32(v), 37, SCALE)
     assert np.abs(got - want).max() > tol
+
+
+def test_split_plan_covers_both_paths():
+    # flat path: 32 tokens per split, at most 16 splits (8 with the reference's
+    # 16 x 8 x 130 workspace); round path: 256-token splits
+    assert O.gqa_plan(2048) == (256, 512, 16)
+    assert O.gqa_plan(32768) == (256, 512, 128)
+    assert O.gqa_plan(100) == (256, 100, 4)
+    assert O.gqa_plan(512, split_limit=8) == (256, 256, 8)
+    assert O.gqa_plan(1) == (256, 1, 1)
+
+
+@pytest.mark.parametrize("kv_len", [31, 32, 33, 200, 511, 512, 513])
+def test_flat_path_boundaries_match_fp64(kv_len):
+    """Split edges of the flat path (a full split, a one-token split, the
+    16-split maximum) and the first length past it (round path)."""
+
+    rng = np.random.default_rng([7, kv_len])
+    q = O.f32_to_bf16(rng.standard_normal(2048).astype(F))
+    k = O.f32_to_bf16(rng.standard_normal((2, 600, 128)).astype(F))
+    v = O.f32_to_bf16(rng.standard_normal((2, 600, 128)).astype(F))
+    got = O.bf16_to_f32(O.gqa(q, k, v, kv_len))
+    want = gqa_f64(O.bf16_to_f32(q), O.bf16_to_f32(k), O.bf16_to_f32(v), kv_len, SCALE)
+    assert np.all(np.abs(got - want) <= 2.0 ** -8 * np.abs(want) + 2e-4)
+
+
+@pytest.mark.parametrize("kv_len", [1, 7, 64, 128, 512])
+def test_round_path_at_short_lengths_matches_the_workspace_fixture(kv_len):
+    """flat_max=0 forces the round path (what a capped workspace uses past its
+    flat limit); the reference fixture's tolerance holds for it too."""
+
+    q, k, v, lens, tol = _kat.gqa_workspace_case()
+    got = O.f16_to_f32(O.gqa(q, k, v, kv_len, flat_max=0, dtype="f16"))
+    want = gqa_f64(O.f16_to_f32(q), O.f16_to_f32(k), O.f16_to_f32(v), kv_len, SCALE)
+    assert np.abs(got - want).max() <= tol
+
+
+def test_flat_and_round_paths_agree():
+    rng = np.random.default_rng(9)
+    kv_len = 300
+    q = O.f32_to_bf16(rng.standard_normal(2048).astype(F))
+    k = O.f32_to_bf16(rng.standard_normal((2, kv_len, 128)).astype(F))
+    v = O.f32_to_bf16(rng.standard_normal((2, kv_len, 128)).astype(F))
+    flat = O.bf16_to_f32(O.gqa(q, k, v, kv_len))
+    rnd = O.bf16_to_f32(O.gqa(q, k, v, kv_len, flat_max=0))
+    # different fp32 operation orders, the same attention to bf16 rounding
+    assert np.all(np.abs(flat - rnd) <= 2.0 ** -7 * np.abs(rnd) + 1e-4)
+
+
+def test_planted_dropped_flat_split_fails():
+    """An oracle that lost the last (one-token) split of the flat path is
+    caught by the fp64 check: at kv_len 33 the dropped token is the one with
+    a dominant key."""
+
+    rng = np.random.default_rng(11)
+    q = O.f32_to_bf16(rng.standard_normal(2048).astype(F))
+    k = rng.standard_normal((2, 33, 128)).astype(F)
+    k[:, 32] = 4.0 * np.sign(O.bf16_to_f32(q).reshape(2, 8, 128).mean(axis=1))
+    k = O.f32_to_bf16(k)
+    v = O.f32_to_bf16(rng.standard_normal((2, 33, 128)).astype(F))
+    want = gqa_f64(O.bf16_to_f32(q), O.bf16_to_f32(k), O.bf16_to_f32(v), 33, SCALE)
+    good = O.bf16_to_f32(O.gqa(q, k, v, 33))
+    dropped = O.bf16_to_f32(O.gqa(q, k[:, :32].copy(), v[:, :32].copy(), 32))
+    assert np.all(np.abs(good - want) <= 2.0 ** -8 * np.abs(want) + 2e-4)
+    assert np.abs(dropped - want).max() > 0.1

@@ -31,6 +31,9 @@
 //
 // Either path ends with one (max, sum, acc[128]) partial per split and head.
 // Then, by the number of splits at this L:
+//   * up to defer_max splits (the decode step sets it): the partials are left
+//     for the consumer, the o_proj row kernel, which merges them while its
+//     weight rows stream in -- no ticket, no cross-block wait here;
 //   * one split finishes in place: out = acc*1 / (sum*1), the general
 //     merge formula with weight exp2(0) = 1 (no ticket, no fences);
 //   * up to kInKernelSplits splits: the partial is written and the last block
@@ -62,9 +65,11 @@ constexpr int kGroups = 4 * kGqaWaves;      // 16-lane groups per block
 constexpr int kRoundTokens = 4 * kGroups;   // tokens per round
 constexpr int kHeadsPerGroup = 8;
 constexpr int kDim = 128;
-constexpr int kPartialStride = 2 + kDim;
+constexpr int kPartialStride = kGqaPartialStride;
+static_assert(kPartialStride == 2 + kDim, "partial layout: max, sum, acc[128]");
 constexpr int kInKernelSplits = 16;
-constexpr int kFlatTokens = kGroups;        // flat path: one token per group, one round per split
+constexpr int kFlatTokens = kGqaFlatTokens;  // flat path: one token per group, one round per split
+static_assert(kFlatTokens == kGroups, "flat path: one token per 16-lane group");
 constexpr int kFlatSplits = kInKernelSplits;
 constexpr int kMergeMaxSplits = 1024;
 constexpr int kMergeDims = 16;              // dims per merge block
@@ -76,9 +81,8 @@ __device__ __forceinline__ int64_t read_kv_len(const GqaArgs& a) {
     return L < 0 ? 0 : (L > a.capacity ? a.capacity : L);
 }
 
-// number of splits that hold tokens at kv_len L (flat or round path)
 __device__ __forceinline__ int64_t split_count(const GqaArgs& a, int64_t L) {
-    return L <= a.flat_max ? (L + kFlatTokens - 1) / kFlatTokens : (L + a.chunk - 1) / a.chunk;
+    return gqa_split_count(L, a.flat_max, a.chunk);
 }
 
 // K and V rows of tokens tk .. tk+3 for one lane (dims 8li..8li+7); indices
@@ -455,6 +459,23 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a) {
         }
     }
 
+    float* part = a.partials;
+    if (nsplit <= a.defer_max) {
+        // left for the consumer kernel, which merges in split order exactly
+        // as below; plain stores, visible to the next kernel in the stream
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const int hl = half * 4 + threadIdx.x / kDim;
+            const int d = threadIdx.x % kDim;
+            float* dst = part + ((g * kHeadsPerGroup + hl) * a.max_splits + s) * kPartialStride;
+            dst[2 + d] = av_out[half];
+            if (d == 0) {
+                dst[0] = s_M[hl];
+                dst[1] = s_L[hl];
+            }
+        }
+        return;
+    }
     if (nsplit == 1) {
         // single split: the general merge with weight exp2(M - M) = 1
 #pragma unroll
@@ -469,7 +490,6 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a) {
         return;
     }
 
-    float* part = a.partials;
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
         const int hl = half * 4 + threadIdx.x / kDim;
@@ -651,7 +671,8 @@ hipError_t launch_gqa_decode(Act act, const GqaArgs& a, hipStream_t stream) {
     const int64_t round_splits = (a.capacity + a.chunk - 1) / a.chunk;
     if (a.max_splits <= 0 || a.max_splits > kMergeMaxSplits || a.chunk <= 0 || a.chunk % kRoundTokens != 0 ||
         a.flat_max < 0 || flat_splits > kFlatSplits || a.capacity <= 0 || round_splits > a.max_splits ||
-        flat_splits > a.max_splits) {
+        flat_splits > a.max_splits || a.defer_max < 0 || a.defer_max > kGqaMaxDefer ||
+        a.defer_max > a.max_splits) {
         return hipErrorInvalidValue;
     }
     const dim3 grid(static_cast<unsigned>(a.max_splits), 2);

@@ -20,6 +20,30 @@ enum class Act { kBf16 = 0, kF16 = 1 };
 //   kSwiGlu    : h[r]   = T(silu(gate_r) * up_r)
 enum class RowMode { kGemv = 0, kQkv = 1, kQkvRope = 2, kSwiGlu = 3 };
 
+// Split-KV attention partials (per query head h and split s: max, sum and
+// acc[128] at (h * max_splits + s) * kGqaPartialStride floats) and the split
+// plan they were made with.  The attention kernel leaves them unmerged when
+// the split count at this kv_len is <= defer_max; its consumer merges them.
+constexpr int kGqaPartialStride = 130;
+constexpr int kGqaFlatTokens = 32;   // tokens per split on the flat path
+constexpr int kGqaMaxDefer = 8;      // most splits a consumer merges
+struct AttnSplits {
+    const float* partials = nullptr;
+    uint16_t* out = nullptr;  // optional: receives the merged vector (one block writes it)
+    const int32_t* kv_len_device = nullptr;
+    int32_t kv_len_offset = 0;
+    int64_t capacity = 0;
+    int64_t chunk = 0;
+    int64_t flat_max = 0;
+    int64_t max_splits = 0;
+    int64_t defer_max = 0;
+};
+
+// splits that hold tokens at kv_len L (flat path up to flat_max, else chunks)
+__host__ __device__ inline int64_t gqa_split_count(int64_t L, int64_t flat_max, int64_t chunk) {
+    return L <= flat_max ? (L + kGqaFlatTokens - 1) / kGqaFlatTokens : (L + chunk - 1) / chunk;
+}
+
 struct Nf4RowsArgs {
     const uint16_t* x = nullptr;      // activation [2048], 16-bit
     const uint16_t* gamma = nullptr;  // RMSNorm weight [2048] or null (no norm)
@@ -43,6 +67,9 @@ struct Nf4RowsArgs {
     const int32_t* tokens = nullptr;
     int64_t vocab = 0;
     uint16_t* hidden_out = nullptr;  // receives the gathered row
+    // kGemv: with attn.partials set, x is the attention output merged from
+    // the partials whenever they were left unmerged (else x is read as is)
+    AttnSplits attn;
 };
 
 hipError_t launch_nf4_rows2048(RowMode mode, Act act, const Nf4RowsArgs& args, hipStream_t stream);
@@ -84,6 +111,7 @@ struct GqaArgs {
     int64_t max_splits = 0;        // grid size per KV head
     int64_t chunk = 64;            // tokens per split on the round path
     int64_t flat_max = 0;          // kv_len <= flat_max takes the flat path (kGqaFlatTokens per split)
+    int64_t defer_max = 0;         // <= kGqaMaxDefer: partials left for the consumer up to this many splits
     float qk_scale_log2 = 0.0f;    // scale * log2(e)
 };
 hipError_t launch_gqa_decode(Act act, const GqaArgs& args, hipStream_t stream);

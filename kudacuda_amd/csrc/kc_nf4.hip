@@ -166,9 +166,20 @@ __device__ __forceinline__ void row_epilogue(const Nf4RowsArgs& a, const RowPair
 // re-read the last task's rows and are discarded).  Vector memory returns in
 // issue order, so the norm waits only for the small vectors while the rows
 // stream in, and each task's dot waits only for its own rows.
-template <typename T, RowMode MODE, int TPW>
+//
+// ATTN (kGemv only): x is the output of split-KV attention.  When the
+// partials were left unmerged (split count <= attn.defer_max), thread t
+// merges head t/16, dims 8(t%16)..+7: M = max of the split maxima, weights
+// exp2(m_s - M), sum and acc accumulated in split order, x = T(acc / sum) --
+// the attention kernel's own merge -- into LDS before the block barrier.
+// The kv_len word, the partials and x (used when the attention merged
+// itself) are requested before the weight rows.
+template <typename T, RowMode MODE, int TPW, bool ATTN = false>
 __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs a, int64_t ntasks) {
+    static_assert(!ATTN || MODE == RowMode::kGemv, "attention merge feeds the GEMV only");
+    static_assert(!ATTN || kRowsThreads * 8 == 2048, "one thread per 8 merged outputs");
     __shared__ float cb[16];
+    __shared__ __attribute__((aligned(16))) uint16_t s_xa[ATTN ? 2048 : 8];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t waves_per_block = kRowsThreads / 64;
@@ -189,7 +200,26 @@ __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs 
         tok = tok < 0 ? 0 : (tok >= a.vocab ? a.vocab - 1 : tok);
         x = a.embed + tok * 2048;
     }
-    const bool has_gamma = a.gamma != nullptr;
+    const bool has_gamma = !ATTN && a.gamma != nullptr;
+    int64_t attn_len = 0;
+    float2 pml[ATTN ? kGqaMaxDefer : 1];
+    float2 pv[ATTN ? kGqaMaxDefer : 1][4];
+    if constexpr (ATTN) {
+        // splits past the plan's count re-read split 0 (loads unconditional)
+        attn_len = static_cast<int64_t>(*a.attn.kv_len_device) + a.attn.kv_len_offset;
+        const float* src = a.attn.partials + static_cast<int64_t>(threadIdx.x >> 4) * a.attn.max_splits *
+                                                 kGqaPartialStride;
+        const int d0 = 8 * (threadIdx.x & 15);
+#pragma unroll
+        for (int x = 0; x < kGqaMaxDefer; ++x) {
+            const float* row = src + (x < a.attn.defer_max ? x : 0) * kGqaPartialStride;
+            pml[x] = *reinterpret_cast<const float2*>(row);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                pv[x][j] = *reinterpret_cast<const float2*>(row + 2 + d0 + 2 * j);
+            }
+        }
+    }
     const uint4* xv = reinterpret_cast<const uint4*>(x) + lane * 4;
     const uint4* gv = reinterpret_cast<const uint4*>(has_gamma ? a.gamma : x) + lane * 4;
     uint4 xr[4], gr[4];
@@ -197,9 +227,11 @@ __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs 
     for (int i = 0; i < 4; ++i) {
         xr[i] = xv[i];
     }
+    if constexpr (!ATTN) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        gr[i] = gv[i];
+        for (int i = 0; i < 4; ++i) {
+            gr[i] = gv[i];
+        }
     }
 
     RowPair tasks[TPW];
@@ -220,8 +252,54 @@ __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs 
     }
     __builtin_amdgcn_sched_barrier(0);
 
+    bool merged = false;
+    if constexpr (ATTN) {
+        const int64_t L = attn_len < 0 ? 0 : (attn_len > a.attn.capacity ? a.attn.capacity : attn_len);
+        const int64_t nsplit = gqa_split_count(L, a.attn.flat_max, a.attn.chunk);
+        merged = nsplit >= 1 && nsplit <= a.attn.defer_max;
+        if (merged) {
+            float M = -__builtin_huge_valf();
+#pragma unroll
+            for (int x = 0; x < kGqaMaxDefer; ++x) {
+                M = x < nsplit ? fmaxf(M, pml[x].x) : M;
+            }
+            float lt = 0.0f;
+            float o[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int x = 0; x < kGqaMaxDefer; ++x) {
+                if (x < nsplit) {
+                    const float w = exp2_fixed(pml[x].x - M);
+                    lt = fmaf(pml[x].y, w, lt);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        o[2 * j] = fmaf(pv[x][j].x, w, o[2 * j]);
+                        o[2 * j + 1] = fmaf(pv[x][j].y, w, o[2 * j + 1]);
+                    }
+                }
+            }
+            uint32_t packed[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                packed[j] = static_cast<uint32_t>(T::store(o[2 * j] / lt)) |
+                            (static_cast<uint32_t>(T::store(o[2 * j + 1] / lt)) << 16);
+            }
+            const uint4 xm = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+            reinterpret_cast<uint4*>(s_xa)[threadIdx.x] = xm;
+            if (blockIdx.x == 0 && a.attn.out != nullptr) {
+                reinterpret_cast<uint4*>(a.attn.out)[threadIdx.x] = xm;
+            }
+        }
+    }
     block_codebook_lds(cb);
     __syncthreads();
+    if constexpr (ATTN) {
+        if (merged) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                xr[i] = reinterpret_cast<const uint4*>(s_xa)[lane * 4 + i];
+            }
+        }
+    }
 
     // RMSNorm of the lane's 32 elements against the whole vector
     float xn[32];
@@ -406,6 +484,13 @@ __global__ __launch_bounds__(256) void nf4_dequantize_kernel(const uint8_t* pack
 
 template <typename T, RowMode MODE, int TPW>
 hipError_t launch_rows_tpw(const Nf4RowsArgs& a, int64_t ntasks, int64_t blocks, hipStream_t stream) {
+    if constexpr (MODE == RowMode::kGemv && TPW == 1) {
+        if (a.attn.partials != nullptr) {
+            hipLaunchKernelGGL((nf4_rows2048_kernel<T, MODE, TPW, true>), dim3(static_cast<unsigned>(blocks)),
+                               dim3(kRowsThreads), 0, stream, a, ntasks);
+            return hipGetLastError();
+        }
+    }
     hipLaunchKernelGGL((nf4_rows2048_kernel<T, MODE, TPW>), dim3(static_cast<unsigned>(blocks)), dim3(kRowsThreads),
                        0, stream, a, ntasks);
     return hipGetLastError();
@@ -423,6 +508,15 @@ hipError_t launch_rows_t(const Nf4RowsArgs& a, hipStream_t stream) {
     }
     if (ntasks <= 0) {
         return hipSuccess;
+    }
+    if (a.attn.partials != nullptr) {
+        // the merge runs in the one-task-per-wave GEMV (<= 3072 tasks) only
+        const AttnSplits& at = a.attn;
+        if (MODE != RowMode::kGemv || ntasks > 3072 || a.gamma != nullptr || a.embed != nullptr ||
+            at.kv_len_device == nullptr || at.capacity <= 0 || at.chunk <= 0 || at.max_splits <= 0 ||
+            at.defer_max < 1 || at.defer_max > kGqaMaxDefer || at.defer_max > at.max_splits) {
+            return hipErrorInvalidValue;
+        }
     }
     // at most 3072 waves (12 per CU on 256 CUs); every wave's tasks in flight
     const int64_t waves_per_block = kRowsThreads / 64;

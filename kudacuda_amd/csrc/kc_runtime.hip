@@ -98,6 +98,9 @@ void set_gqa_plan(GqaArgs& a, int64_t capacity, int64_t split_limit) {
     a.max_splits = p.max_splits;
 }
 
+// splits the decode step's attention leaves for o_proj to merge
+int64_t model_defer(int64_t max_splits) { return max_splits < kGqaMaxDefer ? max_splits : kGqaMaxDefer; }
+
 int64_t gqa_workspace(int64_t tokens) { return 16 * gqa_plan(tokens, 0).max_splits * 130; }
 
 const char* const kGfx950Tactics[] = {
@@ -343,6 +346,7 @@ hipError_t model_op(const Model& m, int op, int64_t layer, bool bookkeeping, hip
             a.kv_len_device = ptr<const int32_t>(G[KUDACUDA_QWEN2_CONTROL]);
             a.kv_len_offset = 1;
             set_gqa_plan(a, m.capacity, 0);
+            a.defer_max = model_defer(a.max_splits);  // o_proj merges these
             a.qk_scale_log2 = static_cast<float>(1.0 / std::sqrt(128.0)) * kLog2e;
             return launch_gqa_decode(Act::kBf16, a, stream);
         }
@@ -354,6 +358,18 @@ hipError_t model_op(const Model& m, int op, int64_t layer, bool bookkeeping, hip
             a.out[0] = ptr<uint16_t>(G[KUDACUDA_QWEN2_HIDDEN]);
             a.residual = ptr<const uint16_t>(G[KUDACUDA_QWEN2_HIDDEN]);
             a.rows[0] = 2048;
+            // attention output: merged here from the partials op 1 left
+            GqaArgs plan;
+            set_gqa_plan(plan, m.capacity, 0);
+            a.attn.partials = ptr<const float>(G[KUDACUDA_QWEN2_ATTN_PARTIALS]);
+            a.attn.out = ptr<uint16_t>(G[KUDACUDA_QWEN2_ATTN]);
+            a.attn.kv_len_device = ptr<const int32_t>(G[KUDACUDA_QWEN2_CONTROL]);
+            a.attn.kv_len_offset = 1;
+            a.attn.capacity = plan.capacity;
+            a.attn.chunk = plan.chunk;
+            a.attn.flat_max = plan.flat_max;
+            a.attn.max_splits = plan.max_splits;
+            a.attn.defer_max = model_defer(plan.max_splits);
             return launch_nf4_rows2048(RowMode::kGemv, Act::kBf16, a, stream);
         }
         case 3: {

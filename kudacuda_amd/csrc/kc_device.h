@@ -118,6 +118,13 @@ __device__ __forceinline__ float row_ror(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 | N, 0xf, 0xf, false));
 }
 
+// DPP row broadcast (row_newbcast:N): every lane of a 16-lane row receives
+// lane N of its row.
+template <int N>
+__device__ __forceinline__ float row_bcast(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 | N, 0xf, 0xf, false));
+}
+
 // Butterfly over the 16 lanes of a row: v += partner for partner distance
 // 8, 4, 2, 1.  Implemented with row rotations: after the distance-8 stage the
 // row holds a period-8 pattern, after distance 4 a period-4 one, ..., so a

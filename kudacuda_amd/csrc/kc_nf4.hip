@@ -263,12 +263,31 @@ __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs 
             for (int x = 0; x < kGqaMaxDefer; ++x) {
                 M = x < nsplit ? fmaxf(M, pml[x].x) : M;
             }
+            // the 16 threads of a head form one DPP row: lane x of the row
+            // evaluates exp2(m_x - M) once and row broadcasts hand it out
+            const int ri = threadIdx.x & 15;
+            float mi = pml[0].x;
+#pragma unroll
+            for (int x = 1; x < kGqaMaxDefer; ++x) {
+                mi = ri == x ? pml[x].x : mi;
+            }
+            const float wi = exp2_fixed(mi - M);
+            float wx[kGqaMaxDefer];
+            wx[0] = row_bcast<0>(wi);
+            wx[1] = row_bcast<1>(wi);
+            wx[2] = row_bcast<2>(wi);
+            wx[3] = row_bcast<3>(wi);
+            wx[4] = row_bcast<4>(wi);
+            wx[5] = row_bcast<5>(wi);
+            wx[6] = row_bcast<6>(wi);
+            wx[7] = row_bcast<7>(wi);
+            static_assert(kGqaMaxDefer == 8, "one broadcast per deferred split");
             float lt = 0.0f;
             float o[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int x = 0; x < kGqaMaxDefer; ++x) {
                 if (x < nsplit) {
-                    const float w = exp2_fixed(pml[x].x - M);
+                    const float w = wx[x];
                     lt = fmaf(pml[x].y, w, lt);
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {

@@ -24,6 +24,11 @@ namespace kc {
 namespace {
 
 constexpr int kRowsThreads = 256;
+// Row-kernel launch cap: up to 6144 waves (24 per CU on 256 CUs), so a
+// wave owns at most 2 tasks of the 11008-task gate/up and the rest own 1;
+// measured faster than fewer waves with more tasks each (the dequant is
+// VALU-heavy and more resident waves hide its LDS and memory latency).
+constexpr int64_t kMaxRowWaves = 6144;
 
 // Decision points between adjacent codebook values: fp32 of the fp64
 // midpoint.  A scaled value s maps to the number of midpoints it exceeds, so
@@ -529,18 +534,17 @@ hipError_t launch_rows_t(const Nf4RowsArgs& a, hipStream_t stream) {
         return hipSuccess;
     }
     if (a.attn.partials != nullptr) {
-        // the merge runs in the one-task-per-wave GEMV (<= 3072 tasks) only
+        // the merge runs in the one-task-per-wave GEMV only
         const AttnSplits& at = a.attn;
-        if (MODE != RowMode::kGemv || ntasks > 3072 || a.gamma != nullptr || a.embed != nullptr ||
+        if (MODE != RowMode::kGemv || ntasks > kMaxRowWaves || a.gamma != nullptr || a.embed != nullptr ||
             at.kv_len_device == nullptr || at.capacity <= 0 || at.chunk <= 0 || at.max_splits <= 0 ||
             at.defer_max < 1 || at.defer_max > kGqaMaxDefer || at.defer_max > at.max_splits) {
             return hipErrorInvalidValue;
         }
     }
-    // at most 3072 waves (12 per CU on 256 CUs); every wave's tasks in flight
+    // every wave's tasks in flight at once
     const int64_t waves_per_block = kRowsThreads / 64;
-    const int64_t max_waves = 3072;
-    int64_t tpw = (ntasks + max_waves - 1) / max_waves;
+    int64_t tpw = (ntasks + kMaxRowWaves - 1) / kMaxRowWaves;
     tpw = tpw <= 1 ? 1 : (tpw <= 2 ? 2 : (tpw <= 4 ? 4 : 8));
     const int64_t waves = (ntasks + tpw - 1) / tpw;
     const int64_t blocks = (waves + waves_per_block - 1) / waves_per_block;
@@ -579,7 +583,7 @@ hipError_t launch_nf4_rows2048(RowMode mode, Act act, const Nf4RowsArgs& a, hipS
 
 hipError_t launch_nf4_down11008(Act act, const Nf4DownArgs& a, hipStream_t stream) {
     constexpr int kChunks = 11008 / 32;
-    constexpr int kRows = 4;
+    constexpr int kRows = 2;  // 1024 blocks of 6 waves: measured faster than 4 or 8 rows per block
     constexpr int kThreads = 64 * ((kChunks + 63) / 64);
     if (a.rows <= 0) {
         return hipSuccess;

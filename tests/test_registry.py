@@ -1,0 +1,49 @@
+"""The module registry of include/kudacuda_registry.h (reference
+include/kudacuda_registry.h:10-41, runtime/kudacuda_registry.cu:33-115),
+exercised by the native smoke program tests/native/registry_smoke."""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+HERE = Path(__file__).resolve().parent
+SMOKE = HERE / "native" / "registry_smoke"
+PROBE = HERE / "native" / "registry_probe.hsaco"
+LIB = HERE.parent / "kudacuda_amd" / "libkudacuda.so"
+
+
+def _built() -> None:
+    if not (SMOKE.exists() and PROBE.exists()):
+        pytest.skip("native smokes not built (python tests/native/build.py)")
+
+
+@pytest.mark.skipif(shutil.which("nm") is None, reason="binutils nm not available")
+def test_library_exports_the_registry_class():
+    out = subprocess.run(["nm", "-DC", "--defined-only", str(LIB)], check=True, capture_output=True,
+                         text=True).stdout
+    for member in ("KudaCudaModuleRegistry::KudaCudaModuleRegistry(int)",
+                   "KudaCudaModuleRegistry::~KudaCudaModuleRegistry()", "KudaCudaModuleRegistry::load(",
+                   "KudaCudaModuleRegistry::resolve(", "KudaCudaModuleRegistry::freeze("):
+        assert f"kudacuda::{member}" in out, member
+
+
+@pytest.mark.skipif(os.path.exists("/dev/kfd"), reason="a GPU is present: the device path is tested instead")
+def test_registry_without_a_device_refuses_every_call():
+    _built()
+    run = subprocess.run([str(SMOKE), "--no-device"], capture_output=True, text=True, timeout=120)
+    assert run.returncode == 0, run.stderr
+    assert "registry smoke ok (no device)" in run.stdout
+
+
+@pytest.mark.gpu
+def test_registry_loads_resolves_launches_and_freezes():
+    _built()
+    print(f"registry smoke: {SMOKE} {PROBE}", flush=True)
+    run = subprocess.run([str(SMOKE), str(PROBE)], capture_output=True, text=True, timeout=120)
+    assert run.returncode == 0, run.stdout + run.stderr
+    assert "registry smoke ok (1000 outputs via probe_affine)" in run.stdout

@@ -15,7 +15,8 @@
 // V rows staged in LDS.  Short caches thus spread over up to 32 CUs instead of
 // running a long per-group chain on 2.
 //
-// Round path (longer L): split s owns tokens [s*C, min(s*C+C, L)).  Per
+// Round path (longer L): split s owns tokens [s*C, min(s*C+C, L)), C = 128
+// up to mid_max and `chunk` (256) beyond, both chosen from L on the device.  Per
 // 128-token round, group gi takes tokens base + 4gi + {0..3}: 8 dot products
 // of 8 dims per lane and a 16-lane butterfly (DPP) give every lane of the group
 // all 32 (token, head) scores (log2 domain: pre-multiplied by scale*log2e).
@@ -82,7 +83,7 @@ __device__ __forceinline__ int64_t read_kv_len(const GqaArgs& a) {
 }
 
 __device__ __forceinline__ int64_t split_count(const GqaArgs& a, int64_t L) {
-    return gqa_split_count(L, a.flat_max, a.chunk);
+    return gqa_split_count(L, a.flat_max, a.mid_max, a.chunk);
 }
 
 // K and V rows of tokens tk .. tk+3 for one lane (dims 8li..8li+7); indices
@@ -119,10 +120,8 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a) {
     const int wave = threadIdx.x >> 6;
     const int gi = wave * 4 + (lane >> 4);
     const int li = lane & 15;
-    const int64_t C = a.chunk;
     const uint16_t* kbase = a.k + static_cast<int64_t>(g) * a.capacity * kDim + 8 * li;
     const uint16_t* vbase = a.v + static_cast<int64_t>(g) * a.capacity * kDim + 8 * li;
-    const int64_t t0 = s * C;
 
     // q does not depend on kv_len: request it first.  Split 0 always exists
     // once kv_len >= 1, so its first rows (bounded by the capacity) are also
@@ -149,6 +148,8 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a) {
     if (s >= nsplit) {
         return;
     }
+    const int64_t C = gqa_split_tokens(L, a.flat_max, a.mid_max, a.chunk);
+    const int64_t t0 = s * C;
 
     float q[kHeadsPerGroup][8];
 #pragma unroll
@@ -646,33 +647,49 @@ __global__ __launch_bounds__(256) void gqa_merge_kernel(GqaArgs a) {
 
 }  // namespace
 
+// Split rule (measured on MI355X): flat path up to 16 x 32 tokens; round
+// path with 128-token splits up to 8192 tokens (more blocks at mid lengths:
+// 1024 tokens 15.9 -> 13.7 us, 8192 tokens 17.7 -> 15.3 us), 256-token splits
+// beyond (at 32768 tokens 256 splits of 128 cost more in the merge than they
+// save: 30.4 vs 22.1 us).
+constexpr int64_t kMidMax = 8192;
+static_assert(kGqaMidTokens == kRoundTokens, "mid-length splits are one round");
+
 int64_t gqa_chunk_for(int64_t) { return 2 * kRoundTokens; }
 
 GqaPlan gqa_plan(int64_t capacity, int64_t split_limit) {
     GqaPlan p;
     p.chunk = gqa_chunk_for(capacity);
     int64_t flat_splits = kFlatSplits;
-    if (split_limit > 0 && split_limit < flat_splits) {
-        flat_splits = split_limit;
+    p.mid_max = kMidMax;
+    if (split_limit > 0) {
+        // a caller-sized workspace: no regime may need more splits than it holds
+        flat_splits = split_limit < flat_splits ? split_limit : flat_splits;
+        p.mid_max = kGqaMidTokens * split_limit < p.mid_max ? kGqaMidTokens * split_limit : p.mid_max;
+        const int64_t need = (capacity + split_limit - 1) / split_limit;
+        const int64_t rounded = (need + kRoundTokens - 1) / kRoundTokens * kRoundTokens;
+        p.chunk = rounded > p.chunk ? rounded : p.chunk;
     }
     p.flat_max = flat_splits * kFlatTokens;
-    if (p.flat_max > capacity) {
-        p.flat_max = capacity;
-    }
-    const int64_t round_splits = (capacity + p.chunk - 1) / p.chunk;
+    p.flat_max = p.flat_max < capacity ? p.flat_max : capacity;
+    p.mid_max = p.mid_max < capacity ? p.mid_max : capacity;
     const int64_t flat = (p.flat_max + kFlatTokens - 1) / kFlatTokens;
-    p.max_splits = round_splits > flat ? round_splits : flat;
+    const int64_t mid = (p.mid_max + kGqaMidTokens - 1) / kGqaMidTokens;
+    const int64_t lng = (capacity + p.chunk - 1) / p.chunk;
+    p.max_splits = flat > mid ? flat : mid;
+    p.max_splits = lng > p.max_splits ? lng : p.max_splits;
     return p;
 }
 
 hipError_t launch_gqa_decode(Act act, const GqaArgs& a, hipStream_t stream) {
-    // the grid must cover every split either path can produce
+    // the grid must cover every split any length up to the capacity produces
     const int64_t flat_splits = (a.flat_max + kFlatTokens - 1) / kFlatTokens;
-    const int64_t round_splits = (a.capacity + a.chunk - 1) / a.chunk;
+    const int64_t mid_splits = (a.mid_max + kGqaMidTokens - 1) / kGqaMidTokens;
+    const int64_t long_splits = a.chunk > 0 ? (a.capacity + a.chunk - 1) / a.chunk : 0;
     if (a.max_splits <= 0 || a.max_splits > kMergeMaxSplits || a.chunk <= 0 || a.chunk % kRoundTokens != 0 ||
-        a.flat_max < 0 || flat_splits > kFlatSplits || a.capacity <= 0 || round_splits > a.max_splits ||
-        flat_splits > a.max_splits || a.defer_max < 0 || a.defer_max > kGqaMaxDefer ||
-        a.defer_max > a.max_splits) {
+        a.flat_max < 0 || flat_splits > kFlatSplits || a.mid_max < 0 || a.capacity <= 0 ||
+        flat_splits > a.max_splits || mid_splits > a.max_splits || long_splits > a.max_splits ||
+        a.defer_max < 0 || a.defer_max > kGqaMaxDefer || a.defer_max > a.max_splits) {
         return hipErrorInvalidValue;
     }
     const dim3 grid(static_cast<unsigned>(a.max_splits), 2);

@@ -26,6 +26,7 @@ enum class RowMode { kGemv = 0, kQkv = 1, kQkvRope = 2, kSwiGlu = 3 };
 // the split count at this kv_len is <= defer_max; its consumer merges them.
 constexpr int kGqaPartialStride = 130;
 constexpr int kGqaFlatTokens = 32;   // tokens per split on the flat path
+constexpr int kGqaMidTokens = 128;   // round-path tokens per split up to mid_max
 constexpr int kGqaMaxDefer = 8;      // most splits a consumer merges
 struct AttnSplits {
     const float* partials = nullptr;
@@ -35,13 +36,19 @@ struct AttnSplits {
     int64_t capacity = 0;
     int64_t chunk = 0;
     int64_t flat_max = 0;
+    int64_t mid_max = 0;
     int64_t max_splits = 0;
     int64_t defer_max = 0;
 };
 
-// splits that hold tokens at kv_len L (flat path up to flat_max, else chunks)
-__host__ __device__ inline int64_t gqa_split_count(int64_t L, int64_t flat_max, int64_t chunk) {
-    return L <= flat_max ? (L + kGqaFlatTokens - 1) / kGqaFlatTokens : (L + chunk - 1) / chunk;
+// Tokens per split at kv_len L: flat path (kGqaFlatTokens) up to flat_max,
+// round path with kGqaMidTokens up to mid_max and `chunk` beyond.
+__host__ __device__ inline int64_t gqa_split_tokens(int64_t L, int64_t flat_max, int64_t mid_max, int64_t chunk) {
+    return L <= flat_max ? kGqaFlatTokens : (L <= mid_max ? kGqaMidTokens : chunk);
+}
+__host__ __device__ inline int64_t gqa_split_count(int64_t L, int64_t flat_max, int64_t mid_max, int64_t chunk) {
+    const int64_t c = gqa_split_tokens(L, flat_max, mid_max, chunk);
+    return (L + c - 1) / c;
 }
 
 struct Nf4RowsArgs {
@@ -111,6 +118,7 @@ struct GqaArgs {
     int64_t max_splits = 0;        // grid size per KV head
     int64_t chunk = 64;            // tokens per split on the round path
     int64_t flat_max = 0;          // kv_len <= flat_max takes the flat path (kGqaFlatTokens per split)
+    int64_t mid_max = 0;           // flat_max < kv_len <= mid_max: round path, kGqaMidTokens per split
     int64_t defer_max = 0;         // <= kGqaMaxDefer: partials left for the consumer up to this many splits
     float qk_scale_log2 = 0.0f;    // scale * log2(e)
 };
@@ -120,6 +128,7 @@ hipError_t launch_gqa_decode(Act act, const GqaArgs& args, hipStream_t stream);
 struct GqaPlan {
     int64_t chunk = 0;
     int64_t flat_max = 0;
+    int64_t mid_max = 0;
     int64_t max_splits = 0;
 };
 GqaPlan gqa_plan(int64_t capacity, int64_t split_limit);

@@ -260,7 +260,7 @@ __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs 
     bool merged = false;
     if constexpr (ATTN) {
         const int64_t L = attn_len < 0 ? 0 : (attn_len > a.attn.capacity ? a.attn.capacity : attn_len);
-        const int64_t nsplit = gqa_split_count(L, a.attn.flat_max, a.attn.chunk);
+        const int64_t nsplit = gqa_split_count(L, a.attn.flat_max, a.attn.mid_max, a.attn.chunk);
         merged = nsplit >= 1 && nsplit <= a.attn.defer_max;
         if (merged) {
             float M = -__builtin_huge_valf();

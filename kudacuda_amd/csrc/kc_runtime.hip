@@ -95,6 +95,7 @@ void set_gqa_plan(GqaArgs& a, int64_t capacity, int64_t split_limit) {
     a.capacity = capacity;
     a.chunk = p.chunk;
     a.flat_max = p.flat_max;
+    a.mid_max = p.mid_max;
     a.max_splits = p.max_splits;
 }
 
@@ -368,6 +369,7 @@ hipError_t model_op(const Model& m, int op, int64_t layer, bool bookkeeping, hip
             a.attn.capacity = plan.capacity;
             a.attn.chunk = plan.chunk;
             a.attn.flat_max = plan.flat_max;
+            a.attn.mid_max = plan.mid_max;
             a.attn.max_splits = plan.max_splits;
             a.attn.defer_max = model_defer(plan.max_splits);
             return launch_nf4_rows2048(RowMode::kGemv, Act::kBf16, a, stream);

@@ -377,19 +377,34 @@ KCO_API void kco_down11008(int act, const uint16_t* x, const uint8_t* w, const f
 /* tokens per split on the round path for a cache of `tokens` rows */
 KCO_API int64_t kco_gqa_chunk_for(int64_t tokens) { (void)tokens; return 2 * GQA_ROUND; }
 
+/* Round path: GQA_ROUND-token splits up to GQA_MID_MAX, `chunk` beyond. */
+#define GQA_MID_MAX 8192
+
 /* The kernels' split plan for a cache of `capacity` rows (split_limit > 0 caps
- * the splits of the flat path): out = {chunk, flat_max, max_splits}. */
+ * every regime's splits): out = {chunk, flat_max, mid_max, max_splits}. */
 KCO_API void kco_gqa_plan(int64_t capacity, int64_t split_limit, int64_t* plan) {
-    const int64_t chunk = kco_gqa_chunk_for(capacity);
+    int64_t chunk = kco_gqa_chunk_for(capacity);
     int64_t flat_splits = GQA_FLAT_SPLITS;
-    if (split_limit > 0 && split_limit < flat_splits) flat_splits = split_limit;
+    int64_t mid_max = GQA_MID_MAX;
+    if (split_limit > 0) {
+        if (split_limit < flat_splits) flat_splits = split_limit;
+        if (GQA_ROUND * split_limit < mid_max) mid_max = GQA_ROUND * split_limit;
+        const int64_t need = (capacity + split_limit - 1) / split_limit;
+        const int64_t rounded = (need + GQA_ROUND - 1) / GQA_ROUND * GQA_ROUND;
+        if (rounded > chunk) chunk = rounded;
+    }
     int64_t flat_max = flat_splits * GQA_GROUPS;
     if (flat_max > capacity) flat_max = capacity;
-    const int64_t round_splits = (capacity + chunk - 1) / chunk;
+    if (mid_max > capacity) mid_max = capacity;
     const int64_t flat = (flat_max + GQA_GROUPS - 1) / GQA_GROUPS;
+    const int64_t mid = (mid_max + GQA_ROUND - 1) / GQA_ROUND;
+    const int64_t lng = (capacity + chunk - 1) / chunk;
+    int64_t ms = flat > mid ? flat : mid;
+    if (lng > ms) ms = lng;
     plan[0] = chunk;
     plan[1] = flat_max;
-    plan[2] = round_splits > flat ? round_splits : flat;
+    plan[2] = mid_max;
+    plan[3] = ms;
 }
 
 /* 16-lane partial dots of one K row with the 8 query heads of its group,
@@ -406,13 +421,16 @@ static void gqa_scores(int act, const float qf[8][128], const uint16_t* krow, fl
     }
 }
 
-/* q [16,128], caches [2, capacity, 128], kv_len L, round-path chunk C
- * (multiple of GQA_ROUND), flat path for L <= flat_max. */
+/* q [16,128], caches [2, capacity, 128], kv_len L; flat path for
+ * L <= flat_max, else the round path with GQA_ROUND-token splits for
+ * L <= mid_max and `chunk`-token splits (a multiple of GQA_ROUND) beyond. */
 KCO_API void kco_gqa(int act, const uint16_t* q, const uint16_t* kc, const uint16_t* vc, int64_t capacity,
-                     int64_t L, int64_t C, int64_t flat_max, float qk_scale_log2, uint16_t* out) {
+                     int64_t L, int64_t chunk, int64_t flat_max, int64_t mid_max, float qk_scale_log2,
+                     uint16_t* out) {
     if (L > capacity) L = capacity;
     if (L < 1) return;
     const int flat = L <= flat_max;
+    const int64_t C = L <= mid_max ? GQA_ROUND : chunk;
     const int64_t nsplit = flat ? (L + GQA_GROUPS - 1) / GQA_GROUPS : (L + C - 1) / C;
     float* part = (float*)malloc(sizeof(float) * 16 * (size_t)nsplit * 130);
 #pragma omp parallel for collapse(2) schedule(static)
@@ -617,7 +635,7 @@ KCO_API void kco_qwen2_step(int64_t num_layers, int64_t vocab, int64_t capacity,
     int64_t L = (int64_t)control[0] + 1;
     if (L > capacity) L = capacity;
     const float qk_scale_log2 = (float)(1.0 / sqrt(128.0)) * kLog2e;
-    int64_t plan[3];
+    int64_t plan[4];
     kco_gqa_plan(capacity, 0, plan);
     for (int64_t layer = 0; layer < num_layers; ++layer) {
         const uint64_t* Lp = layer_ptrs + layer * L_FIELDS;
@@ -629,7 +647,7 @@ KCO_API void kco_qwen2_step(int64_t num_layers, int64_t vocab, int64_t capacity,
                            P(const float*, G[M_ROPE_COS]), P(const float*, G[M_ROPE_SIN]), pos, capacity, query,
                            P(uint16_t*, Lp[L_KEY_CACHE]), P(uint16_t*, Lp[L_VALUE_CACHE]));
         kco_gqa(0, query, P(const uint16_t*, Lp[L_KEY_CACHE]), P(const uint16_t*, Lp[L_VALUE_CACHE]), capacity, L,
-                plan[0], plan[1], qk_scale_log2, attn);
+                plan[0], plan[1], plan[2], qk_scale_log2, attn);
         kco_nf4_gemv2048(0, attn, P(const uint8_t*, Lp[L_O_PACKED]), P(const float*, Lp[L_O_ABSMAX]), NULL, hidden,
                          2048, hidden);
         kco_swiglu(0, hidden, P(const uint16_t*, Lp[L_POST_NORM]), eps, P(const uint8_t*, Lp[L_GATE_PACKED]),

@@ -193,8 +193,10 @@ def test_mlp_config3(torch_gpu, native, stream, with_norm, with_residual):
     _close(host(out), y)
 
 
-# flat path up to 512 (edges 32/33, 511/512), round path beyond (513 ...)
-KV_LENS = [1, 7, 32, 33, 37, 128, 511, 512, 513, 585, 1024, 2048, 8192, 32768]
+# flat path up to 512 (edges 32/33, 511/512); round path beyond with
+# 128-token splits up to 8192 (ticket merge up to 2048 = 16 splits, merge
+# kernel from 2049) and 256-token splits past it (8193, 32768)
+KV_LENS = [1, 7, 32, 33, 37, 128, 511, 512, 513, 585, 1024, 2048, 2049, 8192, 8193, 32768]
 
 
 @pytest.mark.parametrize("kv_len", KV_LENS)

@@ -75,7 +75,7 @@ def test_split_size_changes_only_rounding(chunk):
     q = O.f32_to_bf16(rng.standard_normal(2048).astype(F))
     k = O.f32_to_bf16(rng.standard_normal((2, 2048, 128)).astype(F))
     v = O.f32_to_bf16(rng.standard_normal((2, 2048, 128)).astype(F))
-    got = O.bf16_to_f32(O.gqa(q, k, v, kv_len, chunk=chunk))
+    got = O.bf16_to_f32(O.gqa(q, k, v, kv_len, chunk=chunk, mid_max=0))
     want = gqa_f64(O.bf16_to_f32(q), O.bf16_to_f32(k), O.bf16_to_f32(v), kv_len, SCALE)
     assert np.all(np.abs(got - want) <= 2.0 ** -7 * np.abs(want) + 2e-4)
 
@@ -89,20 +89,26 @@ def test_planted_wrong_group_mapping_fails():
     assert np.abs(got - want).max() > tol
 
 
-def test_split_plan_covers_both_paths():
-    # flat path: 32 tokens per split, at most 16 splits (8 with the reference's
-    # 16 x 8 x 130 workspace); round path: 256-token splits
-    assert O.gqa_plan(2048) == (256, 512, 16)
-    assert O.gqa_plan(32768) == (256, 512, 128)
-    assert O.gqa_plan(100) == (256, 100, 4)
-    assert O.gqa_plan(512, split_limit=8) == (256, 256, 8)
-    assert O.gqa_plan(1) == (256, 1, 1)
+def test_split_plan_covers_every_regime():
+    # (chunk, flat_max, mid_max, max_splits): flat path with 32-token splits up
+    # to 16 x 32 tokens (8 x 32 with the reference's 16 x 8 x 130 workspace),
+    # round path with 128-token splits up to 8192 tokens, 256-token beyond
+    assert O.gqa_plan(2048) == (256, 512, 2048, 16)
+    assert O.gqa_plan(32768) == (256, 512, 8192, 128)
+    assert O.gqa_plan(65536) == (256, 512, 8192, 256)
+    assert O.gqa_plan(100) == (256, 100, 100, 4)
+    assert O.gqa_plan(512, split_limit=8) == (256, 256, 512, 8)
+    assert O.gqa_plan(1) == (256, 1, 1, 1)
+    # a capped workspace also caps the long splits' count
+    chunk, _, mid_max, splits = O.gqa_plan(32768, split_limit=8)
+    assert splits == 8 and chunk * 8 >= 32768 and mid_max == 1024
 
 
-@pytest.mark.parametrize("kv_len", [31, 32, 33, 200, 511, 512, 513])
+@pytest.mark.parametrize("kv_len", [31, 32, 33, 200, 511, 512, 513, 600])
 def test_flat_path_boundaries_match_fp64(kv_len):
     """Split edges of the flat path (a full split, a one-token split, the
-    16-split maximum) and the first length past it (round path)."""
+    16-split maximum) and the first lengths past it (round path, 128-token
+    splits)."""
 
     rng = np.random.default_rng([7, kv_len])
     q = O.f32_to_bf16(rng.standard_normal(2048).astype(F))
@@ -114,12 +120,14 @@ def test_flat_path_boundaries_match_fp64(kv_len):
 
 
 @pytest.mark.parametrize("kv_len", [1, 7, 64, 128, 512])
-def test_round_path_at_short_lengths_matches_the_workspace_fixture(kv_len):
-    """flat_max=0 forces the round path (what a capped workspace uses past its
-    flat limit); the reference fixture's tolerance holds for it too."""
+@pytest.mark.parametrize("regime", [dict(flat_max=0), dict(flat_max=0, mid_max=0)])
+def test_round_path_at_short_lengths_matches_the_workspace_fixture(kv_len, regime):
+    """flat_max=0 forces the round path with 128-token splits (what a capped
+    workspace uses past its flat limit), mid_max=0 too its 256-token splits;
+    the reference fixture's tolerance holds for both."""
 
     q, k, v, lens, tol = _kat.gqa_workspace_case()
-    got = O.f16_to_f32(O.gqa(q, k, v, kv_len, flat_max=0, dtype="f16"))
+    got = O.f16_to_f32(O.gqa(q, k, v, kv_len, dtype="f16", **regime))
     want = gqa_f64(O.f16_to_f32(q), O.f16_to_f32(k), O.f16_to_f32(v), kv_len, SCALE)
     assert np.abs(got - want).max() <= tol
 

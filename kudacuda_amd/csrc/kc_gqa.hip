@@ -37,16 +37,17 @@
 //     weight rows stream in -- no ticket, no cross-block wait here;
 //   * one split finishes in place: out = acc*1 / (sum*1), the general
 //     merge formula with weight exp2(0) = 1 (no ticket, no fences);
-//   * up to kInKernelSplits splits: the partial is written and the last block
-//     of the KV head to finish (device-scope ticket, reset by that block, so
-//     the launch is capture-safe) merges the splits;
+//   * up to ticket_max (<= kInKernelSplits) splits: the partial is written
+//     and the last block of the KV head to finish (a ticket of agent-scope
+//     atomics, reset by that block, so the launch is capture-safe) merges the
+//     splits;
 //   * more splits: the partials are merged by gqa_merge_kernel (grid: query
 //     head x 16-dim slice; partials staged through LDS in one pass), which is
 //     launched after the partial kernel whenever the grid allows more than
-//     kInKernelSplits splits and returns at once when L needs fewer.
+//     ticket_max splits and returns at once when L needs fewer.
 // Every merge sums the splits in index order with the same operations, so the
-// result depends only on (inputs, kv_len, C, flat_max).  kv_len may come from
-// device memory (graph replay); C and flat_max come from the cache length
+// result depends only on (inputs, kv_len, the split rule).  kv_len may come
+// from device memory (graph replay); the rule's bounds come from the cache length
 // (gqa_plan), so a direct call and a graph replay at the same L agree.
 //
 // Math follows the reference's split-KV workspace kernels
@@ -71,7 +72,7 @@ static_assert(kPartialStride == 2 + kDim, "partial layout: max, sum, acc[128]");
 constexpr int kInKernelSplits = 16;
 constexpr int kFlatTokens = kGqaFlatTokens;  // flat path: one token per group, one round per split
 static_assert(kFlatTokens == kGroups, "flat path: one token per 16-lane group");
-constexpr int kFlatSplits = kInKernelSplits;
+constexpr int kFlatSplits = 16;
 constexpr int kMergeMaxSplits = 1024;
 constexpr int kMergeDims = 16;              // dims per merge block
 constexpr int kSlot = 40;                   // per-group LDS exchange: 32 scores + 8 rescales
@@ -502,7 +503,7 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a) {
             store_agent(dst + 1, s_L[hl]);
         }
     }
-    if (nsplit > kInKernelSplits) {
+    if (nsplit > a.ticket_max) {
         return;  // gqa_merge_kernel follows
     }
 
@@ -574,7 +575,7 @@ __global__ __launch_bounds__(256) void gqa_merge_kernel(GqaArgs a) {
     const int d0 = blockIdx.y * kMergeDims;
     const int64_t L = read_kv_len(a);
     const int nsplit = static_cast<int>(split_count(a, L));
-    if (nsplit <= kInKernelSplits) {
+    if (nsplit <= a.ticket_max) {
         return;  // merged by the partial kernel
     }
     const float* src = a.partials + static_cast<int64_t>(h) * a.max_splits * kPartialStride;
@@ -689,7 +690,8 @@ hipError_t launch_gqa_decode(Act act, const GqaArgs& a, hipStream_t stream) {
     if (a.max_splits <= 0 || a.max_splits > kMergeMaxSplits || a.chunk <= 0 || a.chunk % kRoundTokens != 0 ||
         a.flat_max < 0 || flat_splits > kFlatSplits || a.mid_max < 0 || a.capacity <= 0 ||
         flat_splits > a.max_splits || mid_splits > a.max_splits || long_splits > a.max_splits ||
-        a.defer_max < 0 || a.defer_max > kGqaMaxDefer || a.defer_max > a.max_splits) {
+        a.defer_max < 0 || a.defer_max > kGqaMaxDefer || a.defer_max > a.max_splits || a.ticket_max < 1 ||
+        a.ticket_max > kInKernelSplits) {
         return hipErrorInvalidValue;
     }
     const dim3 grid(static_cast<unsigned>(a.max_splits), 2);
@@ -699,7 +701,7 @@ hipError_t launch_gqa_decode(Act act, const GqaArgs& a, hipStream_t stream) {
         hipLaunchKernelGGL(gqa_partial_kernel<F16>, grid, dim3(kGqaThreads), 0, stream, a);
     }
     hipError_t status = hipGetLastError();
-    if (status != hipSuccess || a.max_splits <= kInKernelSplits) {
+    if (status != hipSuccess || a.max_splits <= a.ticket_max) {
         return status;
     }
     const dim3 mgrid(16, kDim / kMergeDims);

@@ -143,6 +143,30 @@ KUDACUDA_API int kudacuda_nf4_gemv_bf16(void* handle, uint64_t input, uint64_t w
                                         int64_t in_features, int64_t out_features, int64_t blocksize,
                                         uint64_t stream);
 
+/* ------------------------------------------------------- NF4 GEMM (prefill) */
+/* NEW — multi-token NF4 GEMM on MFMA for prefill (the reference runs prompt
+ * tokens through bitsandbytes' dequantize + bf16 matmul in the framework,
+ * python/kudacuda_sidecar.py:1719-1738, or as sequential decode steps,
+ * README.md:170).  output[m, n] = bf16(x[m] . Wbf16[n] + bias[n]) or, with
+ * residual (then bias must be 0), bf16(residual[m, n] + bf16(x[m] . Wbf16[n]))
+ * with Wbf16 = bf16(codebook[code] * absmax); fp32 accumulation.  residual may
+ * alias output.  Contract: tokens>=1 (any count; processed 64 at a time),
+ * out_features a positive multiple of 64, in_features a positive multiple of
+ * 128, blocksize=64; x and output row-major [tokens, features] bf16. */
+KUDACUDA_API int kudacuda_nf4_gemm_bf16(void* handle, uint64_t input, uint64_t weight_packed, uint64_t absmax,
+                                        uint64_t bias, uint64_t residual, uint64_t output, int64_t tokens,
+                                        int64_t in_features, int64_t out_features, int64_t blocksize,
+                                        uint64_t stream);
+
+/* NEW — gate/up SwiGLU over many tokens on MFMA: output[m, n] =
+ * bf16(silu(x[m] . Gbf16[n]) * (x[m] . Ubf16[n])), the multi-token form of
+ * kudacuda_qwen2_swiglu_nf4_bf16 (include/kudacuda.h reference :157).  Same
+ * contract as kudacuda_nf4_gemm_bf16. */
+KUDACUDA_API int kudacuda_nf4_gemm_swiglu_bf16(void* handle, uint64_t input, uint64_t gate_weight_packed,
+                                               uint64_t gate_absmax, uint64_t up_weight_packed, uint64_t up_absmax,
+                                               uint64_t output, int64_t tokens, int64_t in_features,
+                                               int64_t out_features, int64_t blocksize, uint64_t stream);
+
 /* NEW — blockwise NF4 quantisation (blocksize 64) of `count` elements of
  * fp32 (input_dtype 0) or bf16 (input_dtype 1); count % 64 == 0.  Replaces
  * bitsandbytes' quantize_4bit for synthetic models (parity with bitsandbytes

@@ -47,6 +47,8 @@ SIGNATURES: dict[str, tuple[list[Any], Any]] = {
     "kudacuda_qwen2_swiglu_nf4_bf16": ([_vp] + [_u64] * 7 + [_i64] * 4 + [_f, _u64], _i),
     "kudacuda_qwen2_mlp_nf4_bf16": ([_vp] + [_u64] * 11 + [_i64] * 4 + [_f, _u64], _i),
     "kudacuda_nf4_gemv_bf16": ([_vp] + [_u64] * 6 + [_i64] * 4 + [_u64], _i),
+    "kudacuda_nf4_gemm_bf16": ([_vp] + [_u64] * 6 + [_i64] * 4 + [_u64], _i),
+    "kudacuda_nf4_gemm_swiglu_bf16": ([_vp] + [_u64] * 6 + [_i64] * 4 + [_u64], _i),
     "kudacuda_nf4_quantize": ([_vp, _u64, _i64, _i64, _i64, _u64, _u64, _u64], _i),
     "kudacuda_nf4_dequantize": ([_vp, _u64, _u64, _i64, _i64, _i64, _u64, _u64], _i),
     "kudacuda_qwen2_gqa_decode_workspace_v3": ([_vp] + [_u64] * 6 + [_i64] * 6 + [_f, _u64], _i),

@@ -93,6 +93,26 @@ struct Nf4DownArgs {
 };
 hipError_t launch_nf4_down11008(Act act, const Nf4DownArgs& args, hipStream_t stream);
 
+// ------------------------------------------------------- prefill (M tokens)
+// NF4 GEMM on MFMA: out[m, n] = epilogue(sum_k x[m, k] * bf16(cb[code] * absmax)),
+// x bf16 [m, k] row-major, weights in the bitsandbytes layout ([n, k/2] codes,
+// [n, k/64] fp32 absmax), fp32 accumulation.  m <= kGemmMaxTokens per launch,
+// n % 64 == 0, k % 128 == 0.
+enum class GemmEpi { kBias = 0, kResidual = 1, kSwiGlu = 2 };
+constexpr int kGemmMaxTokens = 64;
+struct Nf4GemmArgs {
+    const uint16_t* x = nullptr;
+    const uint8_t* w[2] = {nullptr, nullptr};       // kSwiGlu: gate, up
+    const float* absmax[2] = {nullptr, nullptr};
+    const uint16_t* bias = nullptr;      // kBias: [n] (may be null: no bias)
+    const uint16_t* residual = nullptr;  // kResidual: [m, n], may alias out
+    uint16_t* out = nullptr;             // [m, n]
+    int64_t m = 0;
+    int64_t n = 0;
+    int64_t k = 0;
+};
+hipError_t launch_nf4_gemm(GemmEpi epi, const Nf4GemmArgs& args, hipStream_t stream);
+
 // Blockwise NF4 quantisation (blocksize 64) of n elements (n % 64 == 0).
 hipError_t launch_nf4_quantize_f32(const float* src, int64_t n, uint8_t* packed, float* absmax, hipStream_t stream);
 hipError_t launch_nf4_quantize_bf16(const uint16_t* src, int64_t n, uint8_t* packed, float* absmax, hipStream_t stream);

@@ -769,6 +769,102 @@ int kudacuda_nf4_gemv_bf16(void* raw, uint64_t input, uint64_t weight_packed, ui
     return finish(h, symbol, kc::launch_nf4_rows2048(kc::RowMode::kGemv, Act::kBf16, a, as_stream(stream)));
 }
 
+namespace kc {
+namespace {
+
+bool gemm_shape_ok(Handle* h, const char* symbol, int64_t tokens, int64_t in_features, int64_t out_features,
+                   int64_t blocksize) {
+    if (tokens < 1 || in_features < 128 || in_features % 128 != 0 || out_features < 64 || out_features % 64 != 0 ||
+        blocksize != 64) {
+        h->set_error(std::string(symbol) +
+                     " requires tokens>=1, in_features a positive multiple of 128, out_features a positive "
+                     "multiple of 64, and blocksize=64");
+        return false;
+    }
+    return true;
+}
+
+// tokens in launches of kGemmMaxTokens rows
+hipError_t gemm_chunks(GemmEpi epi, Nf4GemmArgs a, int64_t tokens, hipStream_t stream) {
+    const uint16_t* x = a.x;
+    const uint16_t* res = a.residual;
+    uint16_t* out = a.out;
+    for (int64_t m0 = 0; m0 < tokens; m0 += kGemmMaxTokens) {
+        a.m = tokens - m0 < kGemmMaxTokens ? tokens - m0 : kGemmMaxTokens;
+        a.x = x + m0 * a.k;
+        a.residual = res != nullptr ? res + m0 * a.n : nullptr;
+        a.out = out + m0 * a.n;
+        const hipError_t status = launch_nf4_gemm(epi, a, stream);
+        if (status != hipSuccess) {
+            return status;
+        }
+    }
+    return hipSuccess;
+}
+
+}  // namespace
+}  // namespace kc
+
+int kudacuda_nf4_gemm_bf16(void* raw, uint64_t input, uint64_t weight_packed, uint64_t absmax, uint64_t bias,
+                           uint64_t residual, uint64_t output, int64_t tokens, int64_t in_features,
+                           int64_t out_features, int64_t blocksize, uint64_t stream) {
+    Handle* h = as_handle(raw);
+    const char* symbol = "nf4_gemm_bf16";
+    if (!ready(h, "kudacuda_nf4_gemm_bf16")) {
+        return 1;
+    }
+    if (input == 0 || weight_packed == 0 || absmax == 0 || output == 0) {
+        h->set_error(std::string(symbol) + " requires non-null device pointers");
+        return 1;
+    }
+    if (!kc::gemm_shape_ok(h, symbol, tokens, in_features, out_features, blocksize)) {
+        return 1;
+    }
+    if (bias != 0 && residual != 0) {
+        h->set_error(std::string(symbol) + " takes a bias or a residual, not both");
+        return 1;
+    }
+    kc::Nf4GemmArgs a;
+    a.x = ptr<const uint16_t>(input);
+    a.w[0] = ptr<const uint8_t>(weight_packed);
+    a.absmax[0] = ptr<const float>(absmax);
+    a.bias = ptr<const uint16_t>(bias);
+    a.residual = ptr<const uint16_t>(residual);
+    a.out = ptr<uint16_t>(output);
+    a.n = out_features;
+    a.k = in_features;
+    const kc::GemmEpi epi = residual != 0 ? kc::GemmEpi::kResidual : kc::GemmEpi::kBias;
+    return finish(h, symbol, kc::gemm_chunks(epi, a, tokens, as_stream(stream)));
+}
+
+int kudacuda_nf4_gemm_swiglu_bf16(void* raw, uint64_t input, uint64_t gate_weight_packed, uint64_t gate_absmax,
+                                  uint64_t up_weight_packed, uint64_t up_absmax, uint64_t output, int64_t tokens,
+                                  int64_t in_features, int64_t out_features, int64_t blocksize, uint64_t stream) {
+    Handle* h = as_handle(raw);
+    const char* symbol = "nf4_gemm_swiglu_bf16";
+    if (!ready(h, "kudacuda_nf4_gemm_swiglu_bf16")) {
+        return 1;
+    }
+    if (input == 0 || gate_weight_packed == 0 || gate_absmax == 0 || up_weight_packed == 0 || up_absmax == 0 ||
+        output == 0) {
+        h->set_error(std::string(symbol) + " requires non-null device pointers");
+        return 1;
+    }
+    if (!kc::gemm_shape_ok(h, symbol, tokens, in_features, out_features, blocksize)) {
+        return 1;
+    }
+    kc::Nf4GemmArgs a;
+    a.x = ptr<const uint16_t>(input);
+    a.w[0] = ptr<const uint8_t>(gate_weight_packed);
+    a.absmax[0] = ptr<const float>(gate_absmax);
+    a.w[1] = ptr<const uint8_t>(up_weight_packed);
+    a.absmax[1] = ptr<const float>(up_absmax);
+    a.out = ptr<uint16_t>(output);
+    a.n = out_features;
+    a.k = in_features;
+    return finish(h, symbol, kc::gemm_chunks(kc::GemmEpi::kSwiGlu, a, tokens, as_stream(stream)));
+}
+
 int kudacuda_nf4_quantize(void* raw, uint64_t input, int64_t input_dtype, int64_t count, int64_t blocksize,
                           uint64_t packed_output, uint64_t absmax_output, uint64_t stream) {
     Handle* h = as_handle(raw);

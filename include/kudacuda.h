@@ -340,6 +340,20 @@ KUDACUDA_API int kudacuda_qwen2_model_replay(void* model, int64_t steps, uint64_
  * receives the mean launch duration. */
 KUDACUDA_API int kudacuda_qwen2_model_time_op(void* model, int64_t op, int64_t iters, uint64_t stream,
                                               float* avg_ms);
+/* NEW — multi-token prefill (the reference prefills through Transformers or
+ * as one decode step per prompt token, python/kudacuda_static_decode.py:
+ * 271-437, README.md:170): tokens[start .. start+count-1] (device token array)
+ * run through every layer at once (NF4 GEMMs on MFMA with bf16-dequantised
+ * weights, causal GQA over the cache), writing KV cache rows start ..
+ * start+count-1; then the last row's final norm + lm_head + argmax with the
+ * decode bookkeeping (tokens[start+count] = greedy token, step =
+ * start+count), so decode steps / replays continue from there.  workspace:
+ * device memory of kudacuda_qwen2_prefill_workspace_bytes(count) bytes.
+ * Eager (not for capture).  Contract: count>=1, start>=0,
+ * start+count<=kv_capacity. */
+KUDACUDA_API int64_t kudacuda_qwen2_prefill_workspace_bytes(int64_t tokens);
+KUDACUDA_API int kudacuda_qwen2_model_prefill(void* model, uint64_t workspace, int64_t workspace_bytes,
+                                              int64_t start, int64_t count, uint64_t stream);
 KUDACUDA_API void kudacuda_qwen2_model_destroy(void* model);
 
 #ifdef __cplusplus

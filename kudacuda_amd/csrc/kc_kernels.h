@@ -113,6 +113,57 @@ struct Nf4GemmArgs {
 };
 hipError_t launch_nf4_gemm(GemmEpi epi, const Nf4GemmArgs& args, hipStream_t stream);
 
+// Row RMSNorm of m rows of 2048: out[r] = bf16((x[r] * inv_rms) * gamma), the
+// decode kernels' fp32 order.  With `embed`, row r is embed[tokens[start + r]]
+// (token ids clamped to the vocabulary) and is also copied to hidden_out.
+struct PrefillNormArgs {
+    const uint16_t* x = nullptr;
+    const uint16_t* gamma = nullptr;
+    float eps = 1e-6f;
+    const uint16_t* embed = nullptr;
+    const int32_t* tokens = nullptr;
+    const int32_t* control = nullptr;  // control[2] = entries of tokens[] (reads stay below it)
+    int64_t vocab = 0;
+    int64_t start = 0;
+    uint16_t* hidden_out = nullptr;
+    uint16_t* out = nullptr;
+    int64_t m = 0;
+};
+hipError_t launch_prefill_norm(const PrefillNormArgs& args, hipStream_t stream);
+
+// RoPE on q [m, 16, 128] (in place) and k [m, 2, 128] at positions start + r
+// (pairs (d, d + 64), tables [capacity, 64]); k and v rows go to the caches
+// [2, capacity, 128] at those positions.
+struct PrefillRopeArgs {
+    uint16_t* q = nullptr;
+    const uint16_t* k = nullptr;
+    const uint16_t* v = nullptr;
+    const float* rope_cos = nullptr;
+    const float* rope_sin = nullptr;
+    uint16_t* kcache = nullptr;
+    uint16_t* vcache = nullptr;
+    int64_t capacity = 0;
+    int64_t start = 0;
+    int64_t m = 0;
+};
+hipError_t launch_prefill_rope_cache(const PrefillRopeArgs& args, hipStream_t stream);
+
+// Causal GQA attention of m query rows (positions start + r) over cache rows
+// [0, start + r]: out [m, 2048] bf16.
+struct PrefillAttnArgs {
+    const uint16_t* q = nullptr;
+    const uint16_t* kcache = nullptr;
+    const uint16_t* vcache = nullptr;
+    uint16_t* out = nullptr;
+    int64_t capacity = 0;
+    int64_t start = 0;
+    int64_t m = 0;
+    float qk_scale_log2 = 0.0f;
+};
+hipError_t launch_prefill_attention(const PrefillAttnArgs& args, hipStream_t stream);
+// control[0] = step (one vector store; capture-safe)
+hipError_t launch_set_step(int32_t* control, int32_t step, hipStream_t stream);
+
 // Blockwise NF4 quantisation (blocksize 64) of n elements (n % 64 == 0).
 hipError_t launch_nf4_quantize_f32(const float* src, int64_t n, uint8_t* packed, float* absmax, hipStream_t stream);
 hipError_t launch_nf4_quantize_bf16(const uint16_t* src, int64_t n, uint8_t* packed, float* absmax, hipStream_t stream);

@@ -422,6 +422,169 @@ hipError_t model_op(const Model& m, int op, int64_t layer, bool bookkeeping, hip
     }
 }
 
+bool gemm_shape_ok(Handle* h, const char* symbol, int64_t tokens, int64_t in_features, int64_t out_features,
+                   int64_t blocksize) {
+    if (tokens < 1 || in_features < 128 || in_features % 128 != 0 || out_features < 64 || out_features % 64 != 0 ||
+        blocksize != 64) {
+        h->set_error(std::string(symbol) +
+                     " requires tokens>=1, in_features a positive multiple of 128, out_features a positive "
+                     "multiple of 64, and blocksize=64");
+        return false;
+    }
+    return true;
+}
+
+// tokens in launches of kGemmMaxTokens rows
+hipError_t gemm_chunks(GemmEpi epi, Nf4GemmArgs a, int64_t tokens, hipStream_t stream) {
+    const uint16_t* x = a.x;
+    const uint16_t* res = a.residual;
+    uint16_t* out = a.out;
+    for (int64_t m0 = 0; m0 < tokens; m0 += kGemmMaxTokens) {
+        a.m = tokens - m0 < kGemmMaxTokens ? tokens - m0 : kGemmMaxTokens;
+        a.x = x + m0 * a.k;
+        a.residual = res != nullptr ? res + m0 * a.n : nullptr;
+        a.out = out + m0 * a.n;
+        const hipError_t status = launch_nf4_gemm(epi, a, stream);
+        if (status != hipSuccess) {
+            return status;
+        }
+    }
+    return hipSuccess;
+}
+
+// Prefill of `count` tokens at positions start .. start+count-1 (token ids
+// from the device token array) through every layer at once, then the final
+// norm + lm_head + argmax of the last row with the decode bookkeeping
+// (tokens[start+count] = argmax, step = start+count).  Workspace per token:
+// hidden, normalised x, q, k, v, attention output (bf16) and the SwiGLU
+// output (bf16 [11008]).
+constexpr int64_t kPrefillBytesPerToken = (4 * 2048 + 2 * 256 + 11008) * 2;
+
+hipError_t model_prefill(const Model& m, uint8_t* ws, int64_t start, int64_t count, hipStream_t stream) {
+    const auto& G = m.g;
+    uint16_t* hidden = reinterpret_cast<uint16_t*>(ws);
+    uint16_t* xn = hidden + count * 2048;
+    uint16_t* q = xn + count * 2048;
+    uint16_t* k = q + count * 2048;
+    uint16_t* v = k + count * 256;
+    uint16_t* attn = v + count * 256;
+    uint16_t* mlp = attn + count * 2048;
+    const float qk_scale_log2 = static_cast<float>(1.0 / std::sqrt(128.0)) * kLog2e;
+    hipError_t st = hipSuccess;
+    auto gemm = [&](GemmEpi epi, const uint16_t* x, uint64_t w0, uint64_t a0, uint64_t w1, uint64_t a1,
+                    const uint16_t* bias, uint16_t* out, int64_t n, int64_t kdim) {
+        Nf4GemmArgs a;
+        a.x = x;
+        a.w[0] = ptr<const uint8_t>(w0);
+        a.absmax[0] = ptr<const float>(a0);
+        a.w[1] = ptr<const uint8_t>(w1);
+        a.absmax[1] = ptr<const float>(a1);
+        a.bias = bias;
+        a.residual = epi == GemmEpi::kResidual ? out : nullptr;
+        a.out = out;
+        a.n = n;
+        a.k = kdim;
+        return gemm_chunks(epi, a, count, stream);
+    };
+    for (int64_t layer = 0; layer < m.num_layers && st == hipSuccess; ++layer) {
+        const auto& L = m.layers[static_cast<size_t>(layer)];
+        PrefillNormArgs na;
+        na.gamma = ptr<const uint16_t>(L[KUDACUDA_QWEN2_INPUT_NORM]);
+        na.eps = m.eps;
+        na.out = xn;
+        na.m = count;
+        if (layer == 0) {
+            na.embed = ptr<const uint16_t>(G[KUDACUDA_QWEN2_EMBED]);
+            na.tokens = ptr<const int32_t>(G[KUDACUDA_QWEN2_TOKENS]);
+            na.control = ptr<const int32_t>(G[KUDACUDA_QWEN2_CONTROL]);
+            na.vocab = m.vocab;
+            na.start = start;
+            na.hidden_out = hidden;
+        } else {
+            na.x = hidden;
+        }
+        st = launch_prefill_norm(na, stream);
+        if (st == hipSuccess) {
+            st = gemm(GemmEpi::kBias, xn, L[KUDACUDA_QWEN2_Q_PACKED], L[KUDACUDA_QWEN2_Q_ABSMAX], 0, 0,
+                      ptr<const uint16_t>(L[KUDACUDA_QWEN2_Q_BIAS]), q, 2048, 2048);
+        }
+        if (st == hipSuccess) {
+            st = gemm(GemmEpi::kBias, xn, L[KUDACUDA_QWEN2_K_PACKED], L[KUDACUDA_QWEN2_K_ABSMAX], 0, 0,
+                      ptr<const uint16_t>(L[KUDACUDA_QWEN2_K_BIAS]), k, 256, 2048);
+        }
+        if (st == hipSuccess) {
+            st = gemm(GemmEpi::kBias, xn, L[KUDACUDA_QWEN2_V_PACKED], L[KUDACUDA_QWEN2_V_ABSMAX], 0, 0,
+                      ptr<const uint16_t>(L[KUDACUDA_QWEN2_V_BIAS]), v, 256, 2048);
+        }
+        if (st == hipSuccess) {
+            PrefillRopeArgs ra;
+            ra.q = q;
+            ra.k = k;
+            ra.v = v;
+            ra.rope_cos = ptr<const float>(G[KUDACUDA_QWEN2_ROPE_COS]);
+            ra.rope_sin = ptr<const float>(G[KUDACUDA_QWEN2_ROPE_SIN]);
+            ra.kcache = ptr<uint16_t>(L[KUDACUDA_QWEN2_KEY_CACHE]);
+            ra.vcache = ptr<uint16_t>(L[KUDACUDA_QWEN2_VALUE_CACHE]);
+            ra.capacity = m.capacity;
+            ra.start = start;
+            ra.m = count;
+            st = launch_prefill_rope_cache(ra, stream);
+        }
+        if (st == hipSuccess) {
+            PrefillAttnArgs aa;
+            aa.q = q;
+            aa.kcache = ptr<const uint16_t>(L[KUDACUDA_QWEN2_KEY_CACHE]);
+            aa.vcache = ptr<const uint16_t>(L[KUDACUDA_QWEN2_VALUE_CACHE]);
+            aa.out = attn;
+            aa.capacity = m.capacity;
+            aa.start = start;
+            aa.m = count;
+            aa.qk_scale_log2 = qk_scale_log2;
+            st = launch_prefill_attention(aa, stream);
+        }
+        if (st == hipSuccess) {
+            st = gemm(GemmEpi::kResidual, attn, L[KUDACUDA_QWEN2_O_PACKED], L[KUDACUDA_QWEN2_O_ABSMAX], 0, 0,
+                      nullptr, hidden, 2048, 2048);
+        }
+        if (st == hipSuccess) {
+            PrefillNormArgs pa;
+            pa.x = hidden;
+            pa.gamma = ptr<const uint16_t>(L[KUDACUDA_QWEN2_POST_NORM]);
+            pa.eps = m.eps;
+            pa.out = xn;
+            pa.m = count;
+            st = launch_prefill_norm(pa, stream);
+        }
+        if (st == hipSuccess) {
+            st = gemm(GemmEpi::kSwiGlu, xn, L[KUDACUDA_QWEN2_GATE_PACKED], L[KUDACUDA_QWEN2_GATE_ABSMAX],
+                      L[KUDACUDA_QWEN2_UP_PACKED], L[KUDACUDA_QWEN2_UP_ABSMAX], nullptr, mlp, 11008, 2048);
+        }
+        if (st == hipSuccess) {
+            st = gemm(GemmEpi::kResidual, mlp, L[KUDACUDA_QWEN2_DOWN_PACKED], L[KUDACUDA_QWEN2_DOWN_ABSMAX], 0, 0,
+                      nullptr, hidden, 2048, 11008);
+        }
+    }
+    if (st != hipSuccess) {
+        return st;
+    }
+    st = launch_set_step(ptr<int32_t>(G[KUDACUDA_QWEN2_CONTROL]), static_cast<int32_t>(start + count - 1), stream);
+    if (st != hipSuccess) {
+        return st;
+    }
+    LmHeadArgs a;
+    a.x = hidden + (count - 1) * 2048;
+    a.gamma = ptr<const uint16_t>(G[KUDACUDA_QWEN2_FINAL_NORM]);
+    a.eps = m.eps;
+    a.weight = ptr<const uint16_t>(G[KUDACUDA_QWEN2_EMBED]);
+    a.vocab = m.vocab;
+    a.logits = ptr<uint16_t>(G[KUDACUDA_QWEN2_LOGITS]);
+    a.block_best = ptr<float>(G[KUDACUDA_QWEN2_LM_BEST]);
+    a.counter = ptr<uint32_t>(G[KUDACUDA_QWEN2_LM_COUNTER]);
+    a.control = ptr<int32_t>(G[KUDACUDA_QWEN2_CONTROL]);
+    a.tokens = ptr<int32_t>(G[KUDACUDA_QWEN2_TOKENS]);
+    return launch_lm_head_argmax(a, stream);
+}
+
 hipError_t model_step(const Model& m, hipStream_t stream) {
     for (int64_t layer = 0; layer < m.num_layers; ++layer) {
         for (int op = 0; op < 5; ++op) {
@@ -769,41 +932,6 @@ int kudacuda_nf4_gemv_bf16(void* raw, uint64_t input, uint64_t weight_packed, ui
     return finish(h, symbol, kc::launch_nf4_rows2048(kc::RowMode::kGemv, Act::kBf16, a, as_stream(stream)));
 }
 
-namespace kc {
-namespace {
-
-bool gemm_shape_ok(Handle* h, const char* symbol, int64_t tokens, int64_t in_features, int64_t out_features,
-                   int64_t blocksize) {
-    if (tokens < 1 || in_features < 128 || in_features % 128 != 0 || out_features < 64 || out_features % 64 != 0 ||
-        blocksize != 64) {
-        h->set_error(std::string(symbol) +
-                     " requires tokens>=1, in_features a positive multiple of 128, out_features a positive "
-                     "multiple of 64, and blocksize=64");
-        return false;
-    }
-    return true;
-}
-
-// tokens in launches of kGemmMaxTokens rows
-hipError_t gemm_chunks(GemmEpi epi, Nf4GemmArgs a, int64_t tokens, hipStream_t stream) {
-    const uint16_t* x = a.x;
-    const uint16_t* res = a.residual;
-    uint16_t* out = a.out;
-    for (int64_t m0 = 0; m0 < tokens; m0 += kGemmMaxTokens) {
-        a.m = tokens - m0 < kGemmMaxTokens ? tokens - m0 : kGemmMaxTokens;
-        a.x = x + m0 * a.k;
-        a.residual = res != nullptr ? res + m0 * a.n : nullptr;
-        a.out = out + m0 * a.n;
-        const hipError_t status = launch_nf4_gemm(epi, a, stream);
-        if (status != hipSuccess) {
-            return status;
-        }
-    }
-    return hipSuccess;
-}
-
-}  // namespace
-}  // namespace kc
 
 int kudacuda_nf4_gemm_bf16(void* raw, uint64_t input, uint64_t weight_packed, uint64_t absmax, uint64_t bias,
                            uint64_t residual, uint64_t output, int64_t tokens, int64_t in_features,
@@ -1187,6 +1315,32 @@ int kudacuda_qwen2_model_step(void* raw_model, uint64_t stream) {
         return 1;
     }
     return finish(m->handle, "qwen2_model_step", kc::model_step(*m, as_stream(stream)));
+}
+
+int64_t kudacuda_qwen2_prefill_workspace_bytes(int64_t tokens) {
+    return tokens < 1 ? 0 : tokens * kc::kPrefillBytesPerToken;
+}
+
+int kudacuda_qwen2_model_prefill(void* raw_model, uint64_t workspace, int64_t workspace_bytes, int64_t start,
+                                 int64_t count, uint64_t stream) {
+    auto* m = reinterpret_cast<kc::Model*>(raw_model);
+    if (m == nullptr) {
+        return 1;
+    }
+    Handle* h = m->handle;
+    const char* symbol = "qwen2_model_prefill";
+    if (workspace == 0) {
+        h->set_error(std::string(symbol) + " requires a non-null workspace");
+        return 1;
+    }
+    if (count < 1 || start < 0 || start + count > m->capacity ||
+        workspace_bytes < kudacuda_qwen2_prefill_workspace_bytes(count)) {
+        h->set_error(std::string(symbol) +
+                     " requires count>=1, 0<=start, start+count<=kv_capacity and a workspace of "
+                     "kudacuda_qwen2_prefill_workspace_bytes(count) bytes");
+        return 1;
+    }
+    return finish(h, symbol, kc::model_prefill(*m, ptr<uint8_t>(workspace), start, count, as_stream(stream)));
 }
 
 int kudacuda_qwen2_model_capture(void* raw_model, uint64_t stream) {

@@ -120,6 +120,7 @@ class Qwen2Nf4Decoder:
         if not self.model:
             raise NativeError(f"kudacuda_qwen2_model_create failed: {native.error()}")
         self.captured = False
+        self._prefill_ws: Any = None
 
     # ------------------------------------------------------------ building
     @classmethod
@@ -202,6 +203,37 @@ class Qwen2Nf4Decoder:
             raise ValueError("prompt + new tokens exceed the token/KV capacity")
         self.reset(prompt)
         self.run_steps(total - 1, graph=graph)
+        self.stream.synchronize()
+        return self.tokens[prompt.size:total].cpu().numpy().copy()
+
+    def prefill(self, prompt: np.ndarray) -> None:
+        """Load ``prompt`` and run it through the model in one multi-token pass
+        (``kudacuda_qwen2_model_prefill``): KV cache rows 0..P-1 are written,
+        tokens[P] receives the greedy token and the step moves to P, so
+        ``replay``/``step`` continue the decode from there."""
+
+        prompt = np.asarray(prompt, dtype=np.int32)
+        if prompt.size > min(self.token_capacity - 1, self.kv_capacity):
+            raise ValueError("prompt exceeds the token/KV capacity")
+        self.reset(prompt)
+        lib = self.native.lib
+        nbytes = int(lib.kudacuda_qwen2_prefill_workspace_bytes(prompt.size))
+        if self._prefill_ws is None or self._prefill_ws.numel() < nbytes:
+            self._prefill_ws = self.torch.empty(nbytes, dtype=self.torch.uint8, device=self.tokens.device)
+        self.native.check(lib.kudacuda_qwen2_model_prefill(self.model, self._prefill_ws.data_ptr(), nbytes, 0,
+                                                           prompt.size, self.stream.cuda_stream),
+                          "kudacuda_qwen2_model_prefill")
+
+    def generate_prefilled(self, prompt: np.ndarray, new_tokens: int) -> np.ndarray:
+        """``generate`` with a multi-token prefill instead of one decode step
+        per prompt token."""
+
+        prompt = np.asarray(prompt, dtype=np.int32)
+        total = prompt.size + int(new_tokens)
+        if total > min(self.token_capacity, self.kv_capacity + 1):
+            raise ValueError("prompt + new tokens exceed the token/KV capacity")
+        self.prefill(prompt)
+        self.run_steps(total - prompt.size - 1, graph=True)
         self.stream.synchronize()
         return self.tokens[prompt.size:total].cpu().numpy().copy()
 

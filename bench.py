@@ -14,7 +14,9 @@ Also reported: per-kernel mean launch time from HIP events on the decode
 stream (each kernel launched back to back over all 36 layers, so weights are
 not cache resident), the roofline of the kernel that dominates the step, and
 the CPU oracle (oracle/kc_oracle.c, OpenMP) timed on a bounded sample of the
-same decode on this host.
+same decode on this host, and the multi-token prefill of the same 64-token
+prompt (kudacuda_qwen2_model_prefill, HIP events, median of 5) beside the 63
+sequential decode steps the timed region starts after.
 
 Usage: python bench.py [--gpus 1] [--steps 128] [--warmup 16]
 """
@@ -179,6 +181,29 @@ def main(argv: list[str] | None = None) -> int:
         n = min(len(golden["tokens"]), args.steps)
         parity = bool(np.array_equal(tokens[:n], np.asarray(golden["tokens"][:n])))
 
+    # multi-token prefill of the same prompt (all layers at once, MFMA GEMMs)
+    # beside the 63 sequential decode steps the measurement above starts from
+    model.prefill(prompt)  # warm (workspace allocation, code paths)
+    stream.synchronize()
+    prefill_runs = []
+    for _ in range(5):
+        model.reset(prompt)
+        p_start = torch.cuda.Event(enable_timing=True)
+        p_stop = torch.cuda.Event(enable_timing=True)
+        p_start.record(stream)
+        model.prefill(prompt)
+        p_stop.record(stream)
+        p_stop.synchronize()
+        prefill_runs.append(p_start.elapsed_time(p_stop))
+    prefill_ms = float(np.median(prefill_runs))
+    first_token_agrees = bool(int(model.tokens[PROMPT_LEN].item()) == int(tokens[0]))
+    prefill_report = {
+        "tokens": PROMPT_LEN, "ms": round(prefill_ms, 4), "tok_s": round(PROMPT_LEN / (prefill_ms * 1e-3), 1),
+        "sequential_decode_ms": round((PROMPT_LEN - 1) * event_ms / args.steps, 4),
+        "first_token_equals_sequential": first_token_agrees,
+    }
+    print(f"[bench] prefill of {PROMPT_LEN} tokens: {prefill_ms:.3f} ms", file=sys.stderr, flush=True)
+
     # per-kernel timing (HIP events on the decode stream, layers cycled)
     kv_len = PROMPT_LEN + args.steps // 2
     model.set_step(kv_len - 1)
@@ -231,6 +256,7 @@ def main(argv: list[str] | None = None) -> int:
         },
         "step_hbm_gbs": round(step_bytes(cfg, cfg.vocab, kv_len) * value / 1e9, 1),
         "per_kernel": op_report,
+        "prefill": prefill_report,
         "token_parity_vs_oracle": parity,
         "reference_rtx3050_fp16_tok_s": 51.825,
     }

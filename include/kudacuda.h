@@ -348,7 +348,8 @@ KUDACUDA_API int kudacuda_qwen2_model_time_op(void* model, int64_t op, int64_t i
  * start+count-1; then the last row's final norm + lm_head + argmax with the
  * decode bookkeeping (tokens[start+count] = greedy token, step =
  * start+count), so decode steps / replays continue from there.  workspace:
- * device memory of kudacuda_qwen2_prefill_workspace_bytes(count) bytes.
+ * device memory of kudacuda_qwen2_prefill_workspace_bytes(count) bytes
+ * (activations per token plus 16 MiB of split-K scratch for the GEMMs).
  * Eager (not for capture).  Contract: count>=1, start>=0,
  * start+count<=kv_capacity. */
 KUDACUDA_API int64_t kudacuda_qwen2_prefill_workspace_bytes(int64_t tokens);

@@ -100,6 +100,8 @@ hipError_t launch_nf4_down11008(Act act, const Nf4DownArgs& args, hipStream_t st
 // n % 64 == 0, k % 128 == 0.
 enum class GemmEpi { kBias = 0, kResidual = 1, kSwiGlu = 2 };
 constexpr int kGemmMaxTokens = 64;
+// split-K scratch: fp32 partial tiles [weights][splits][m][n]
+constexpr int64_t kGemmScratchFloats = int64_t{4} << 20;
 struct Nf4GemmArgs {
     const uint16_t* x = nullptr;
     const uint8_t* w[2] = {nullptr, nullptr};       // kSwiGlu: gate, up
@@ -110,6 +112,11 @@ struct Nf4GemmArgs {
     int64_t m = 0;
     int64_t n = 0;
     int64_t k = 0;
+    // Split-K scratch (null: one block column per row tile).  With it, K is
+    // split so the launch has ~1024 waves; partial tiles are summed in split
+    // order by a second kernel that applies the epilogue.
+    float* partials = nullptr;
+    int64_t partial_floats = 0;
 };
 hipError_t launch_nf4_gemm(GemmEpi epi, const Nf4GemmArgs& args, hipStream_t stream);
 

@@ -6,19 +6,34 @@
 // python/kudacuda_sidecar.py:1719-1738, kernels/common/nf4_device.cuh:10-40)
 // and fp32 accumulation in v_mfma_f32_16x16x32_bf16.
 //
-// Tiling: a block is 4 waves, a wave owns 16 weight rows (kSwiGlu: 16 gate
-// rows and the same 16 up rows) and all m <= 64 tokens (4 token tiles of
-// 16).  Operand layouts of the 16x16x32 bf16 MFMA (lane l, row l%16, group
+// Tiling: a block is 4 waves and each wave owns one 16-row weight fragment
+// and all m <= 64 tokens (NT token tiles of 16, a template parameter so the
+// window loop is straight-line code).  kBias / kResidual: the block's waves
+// own output rows [n0, n0 + 64).  kSwiGlu: waves 0 and 1 own gate rows
+// [n0, n0 + 32), waves 2 and 3 the same up rows; the up sums reach the gate
+// waves through LDS for the epilogue.
+//
+// Operand layouts of the 16x16x32 bf16 MFMA (lane l, row l%16, group
 // q = l/16): A[l%16][8q + j], B[8q + j][l%16], D[4q + i][l%16].  With
 // A = weights (rows n) and B[k][m] = x[m][k], D[n][m] is the output tile.
 // k is walked in windows of 128: lane group q owns the 32 contiguous k
-// [128w + 32q, 128w + 32q + 32), read as one 16-byte load of codes (and one
-// absmax, the 32 codes sit in one 64-block) per weight row and four 16-byte
-// loads per token row; MFMA step s of the window takes k = 128w + 32q + 8s + j
-// from both operands, so every k of the window is summed exactly once (the
-// order of k inside a product sum does not change what is summed).
-// Activations (m x k bf16, at most 64 x 11008 x 2 B) are read through the
-// caches; the weights stream once.
+// [128w + 32q, 128w + 32q + 32) of its weight row, read as one 16-byte load
+// of codes (and one absmax: the 32 codes sit in one 64-block); MFMA step s of
+// the window takes k = 128w + 32q + 8s + j from both operands, so every k of
+// the window is summed exactly once (the order of k inside a product sum does
+// not change what is summed).
+//
+// Activations: the block stages each window's x tile (16 NT rows x 128 k)
+// in LDS once, with coalesced 16-byte loads (16 lanes cover one 256-byte row
+// slice), rows padded to 272 bytes so that the MFMA operand reads
+// (16 bytes per lane, lanes r = 0..7 of a group on distinct banks) do not
+// conflict; the tile is double-buffered and the next window's x and weights
+// are requested before the current window is computed.
+//
+// Few row tiles (n = 256 .. 2048) would leave most CUs idle, so K is split
+// over a second grid dimension (each block sums a range of windows); the
+// fp32 partial tiles are then summed in split order by gemm_reduce_kernel,
+// which applies the epilogue.
 #include "kc_device.h"
 #include "kc_kernels.h"
 
@@ -34,108 +49,164 @@ constexpr int kRowsPerWave = 16;
 constexpr int kRowsPerBlock = kRowsPerWave * kGemmWaves;
 constexpr int kTokenTiles = kGemmMaxTokens / 16;
 constexpr int kWindow = 128;
+constexpr int kXPitch = kWindow * 2 + 16;  // bytes per staged token row
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 // 8 codes of one 32-bit word (byte b: element 2b in the high nibble, 2b+1 in
-// the low nibble) times absmax, each rounded to bf16; element j lands in
-// 16-bit slot j of the result.
-__device__ __forceinline__ uint4 dequant8_bf16(uint32_t word, float am, const float* cb) {
-    uint32_t out[4];
+// the low nibble) times absmax, each rounded to bf16 (round to nearest even,
+// v_cvt_pk_bf16_f32; the products are finite); element j lands in slot j.
+__device__ __forceinline__ bf16x8 dequant8_bf16(uint32_t word, float am, const float* cb) {
+    bf16x8 v;
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
         const uint32_t byte = (word >> (8 * b)) & 0xffu;
-        const uint32_t hi = f32_to_bf16(cb[byte >> 4] * am);
-        const uint32_t lo = f32_to_bf16(cb[byte & 0xfu] * am);
-        out[b] = hi | (lo << 16);
+        v[2 * b] = static_cast<__bf16>(cb[byte >> 4] * am);
+        v[2 * b + 1] = static_cast<__bf16>(cb[byte & 0xfu] * am);
     }
-    return make_uint4(out[0], out[1], out[2], out[3]);
+    return v;
 }
 
-template <GemmEpi EPI>
+// One window's requests of a thread: its NT 16-byte pieces of the x tile
+// (token row 16j + tid/16, bytes 16 (tid%16) of the row's window slice) and
+// its wave's weight codes (32 per lane) with their absmax.
+template <int NT>
+struct GemmFetch {
+    uint4 x[NT];
+    uint4 w;
+    float am;
+};
+
+template <int NT>
+__device__ __forceinline__ void gemm_fetch(GemmFetch<NT>& o, const uint16_t* const* xrow, int xcol,
+                                           const uint8_t* wrow, const float* arow, int64_t kw, int q) {
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+        o.x[j] = *reinterpret_cast<const uint4*>(xrow[j] + kw + xcol);
+    }
+    const int64_t kq = kw + 32 * q;
+    o.w = *reinterpret_cast<const uint4*>(wrow + kq / 2);
+    o.am = arow[kq / 64];
+}
+
+template <int NT>
+__device__ __forceinline__ void gemm_stage(uint8_t* buf, const GemmFetch<NT>& o, int tid) {
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+        *reinterpret_cast<uint4*>(buf + (16 * j + tid / 16) * kXPitch + 16 * (tid % 16)) = o.x[j];
+    }
+}
+
+template <int NT>
+__device__ __forceinline__ void gemm_window(const uint8_t* buf, const GemmFetch<NT>& o, floatx4* acc, int r, int q,
+                                            const float* cb) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const uint32_t word = s == 0 ? o.w.x : (s == 1 ? o.w.y : (s == 2 ? o.w.z : o.w.w));
+        const bf16x8 A = dequant8_bf16(word, o.am, cb);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const uint4 B = *reinterpret_cast<const uint4*>(buf + (16 * t + r) * kXPitch + 64 * q + 16 * s);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, as_bf16x8(B), acc[t], 0, 0, 0);
+        }
+    }
+}
+
+template <GemmEpi EPI, int NT>
 __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(Nf4GemmArgs a) {
-    constexpr int NF = EPI == GemmEpi::kSwiGlu ? 2 : 1;  // weight fragments per wave
+    constexpr bool kSw = EPI == GemmEpi::kSwiGlu;
+    constexpr int kBlockRows = kSw ? kRowsPerBlock / 2 : kRowsPerBlock;  // output rows of the block
     __shared__ float cb[16];
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    __shared__ __attribute__((aligned(16))) uint8_t s_x[2][16 * NT * kXPitch];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane & 15;
     const int q = lane >> 4;
     const int64_t K = a.k;
-    const int M = static_cast<int>(a.m);
-    const int ntiles = (M + 15) / 16;
-    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + wave * kRowsPerWave;
-    const int64_t nrow = n0 + r;  // n % 64 == 0: every row exists
-
-    const uint8_t* wrow[NF];
-    const float* arow[NF];
+    const int M = static_cast<int>(a.m);  // 16 * (NT - 1) < M <= 16 * NT
+    const int S = static_cast<int>(gridDim.y);
+    const int64_t windows = K / kWindow;
+    const int64_t per_split = (windows + S - 1) / S;
+    const int64_t k_begin = static_cast<int64_t>(blockIdx.y) * per_split * kWindow;
+    const int64_t k_end = k_begin + per_split * kWindow < K ? k_begin + per_split * kWindow : K;
+    // this wave's fragment: f = 0 (gate or plain) / 1 (up), first row n0w
+    const int f = kSw ? wave >> 1 : 0;
+    const int64_t n0w = static_cast<int64_t>(blockIdx.x) * kBlockRows + (kSw ? wave & 1 : wave) * kRowsPerWave;
+    const uint8_t* wrow = a.w[f] + (n0w + r) * (K / 2);  // n % 64 == 0: every row exists
+    const float* arow = a.absmax[f] + (n0w + r) * (K / 64);
+    // x rows this thread stages (rows past m re-read row m - 1; never used)
+    const uint16_t* xrow[NT];
 #pragma unroll
-    for (int f = 0; f < NF; ++f) {
-        wrow[f] = a.w[f] + nrow * (K / 2);
-        arow[f] = a.absmax[f] + nrow * (K / 64);
+    for (int j = 0; j < NT; ++j) {
+        const int m = 16 * j + tid / 16 < M ? 16 * j + tid / 16 : M - 1;
+        xrow[j] = a.x + static_cast<int64_t>(m) * K;
     }
-    // token rows of the B operand (rows past m re-read row m-1; discarded)
-    const uint16_t* xrow[kTokenTiles];
-#pragma unroll
-    for (int t = 0; t < kTokenTiles; ++t) {
-        const int m = 16 * t + r < M ? 16 * t + r : M - 1;
-        xrow[t] = a.x + static_cast<int64_t>(m) * K;
-    }
+    const int xcol = 8 * (tid % 16);
     block_codebook_lds(cb);
+
+    floatx4 acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        acc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    GemmFetch<NT> cur, nxt;
+    gemm_fetch<NT>(cur, xrow, xcol, wrow, arow, k_begin, q);
+    gemm_stage<NT>(s_x[0], cur, tid);
     __syncthreads();
-
-    floatx4 acc[NF][kTokenTiles];
-#pragma unroll
-    for (int f = 0; f < NF; ++f) {
-#pragma unroll
-        for (int t = 0; t < kTokenTiles; ++t) {
-            acc[f][t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-        }
-    }
-    for (int64_t kw = 0; kw < K; kw += kWindow) {
-        const int64_t kq = kw + 32 * q;
-        uint4 wq[NF];
-        float am[NF];
-#pragma unroll
-        for (int f = 0; f < NF; ++f) {
-            wq[f] = *reinterpret_cast<const uint4*>(wrow[f] + kq / 2);
-            am[f] = arow[f][kq / 64];
-        }
-        uint4 xb[kTokenTiles][4];
-#pragma unroll
-        for (int t = 0; t < kTokenTiles; ++t) {
-            if (t < ntiles) {
-#pragma unroll
-                for (int s = 0; s < 4; ++s) {
-                    xb[t][s] = *reinterpret_cast<const uint4*>(xrow[t] + kq + 8 * s);
-                }
-            }
-        }
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-#pragma unroll
-            for (int f = 0; f < NF; ++f) {
-                const uint32_t word = s == 0 ? wq[f].x : (s == 1 ? wq[f].y : (s == 2 ? wq[f].z : wq[f].w));
-                const bf16x8 A = as_bf16x8(dequant8_bf16(word, am[f], cb));
-#pragma unroll
-                for (int t = 0; t < kTokenTiles; ++t) {
-                    if (t < ntiles) {
-                        acc[f][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, as_bf16x8(xb[t][s]), acc[f][t], 0, 0,
-                                                                             0);
-                    }
-                }
-            }
-        }
+    int buf = 0;
+    for (int64_t kw = k_begin; kw < k_end; kw += kWindow) {
+        // the split's last window is requested again and staged unused
+        const int64_t kn = kw + kWindow < k_end ? kw + kWindow : kw;
+        gemm_fetch<NT>(nxt, xrow, xcol, wrow, arow, kn, q);
+        __builtin_amdgcn_sched_barrier(0);  // keep the requests ahead of the compute
+        gemm_window<NT>(s_x[buf], cur, acc, r, q, cb);
+        gemm_stage<NT>(s_x[buf ^ 1], nxt, tid);
+        __syncthreads();
+        cur = nxt;
+        buf ^= 1;
     }
 
-    // D[4q + i][r]: rows n0 + 4q + i, token 16t + r; four consecutive rows per
-    // lane go out as one 8-byte store
+    // D[4q + i][r]: rows n0w + 4q + i, token 16t + r; four consecutive rows
+    // per lane go out as one store
+    if (S > 1) {
 #pragma unroll
-    for (int t = 0; t < kTokenTiles; ++t) {
+        for (int t = 0; t < NT; ++t) {
+            const int m = 16 * t + r;
+            if (m < M) {
+                float* dst = a.partials + ((static_cast<int64_t>(f) * S + blockIdx.y) * M + m) * a.n + n0w + 4 * q;
+                *reinterpret_cast<float4*>(dst) = make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+            }
+        }
+        return;
+    }
+    floatx4 up[NT];
+    if constexpr (kSw) {
+        // the up waves hand their sums to the gate waves of the same rows
+        // (the staging buffers are free: the loop ended on a barrier)
+        floatx4* s_up = reinterpret_cast<floatx4*>(&s_x[0][0]);
+        if (f == 1) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                s_up[((wave & 1) * NT + t) * 64 + lane] = acc[t];
+            }
+        }
+        __syncthreads();
+        if (f == 1) {
+            return;
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            up[t] = s_up[((wave & 1) * NT + t) * 64 + lane];
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
         const int m = 16 * t + r;
-        if (t >= ntiles || m >= M) {
+        if (m >= M) {
             continue;
         }
-        const int64_t nb = n0 + 4 * q;
+        const int64_t nb = n0w + 4 * q;
         uint16_t* dst = a.out + static_cast<int64_t>(m) * a.n + nb;
         uint32_t packed[2];
 #pragma unroll
@@ -144,7 +215,7 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(Nf4GemmArgs a) {
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
                 const int i = 2 * i2 + e;
-                float v = acc[0][t][i];
+                float v = acc[t][i];
                 if constexpr (EPI == GemmEpi::kBias) {
                     if (a.bias != nullptr) {
                         v = v + Bf16::load(a.bias[nb + i]);
@@ -154,14 +225,104 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(Nf4GemmArgs a) {
                     const float res = Bf16::load(a.residual[static_cast<int64_t>(m) * a.n + nb + i]);
                     h[e] = Bf16::store(res + Bf16::load(Bf16::store(v)));
                 } else {
-                    const float u = acc[NF - 1][t][i];
-                    h[e] = Bf16::store(silu_fixed(v) * u);
+                    h[e] = Bf16::store(silu_fixed(v) * up[t][i]);
                 }
             }
             packed[i2] = static_cast<uint32_t>(h[0]) | (static_cast<uint32_t>(h[1]) << 16);
         }
         *reinterpret_cast<uint2*>(dst) = make_uint2(packed[0], packed[1]);
     }
+}
+
+// One thread per 4 consecutive outputs of one token: the split partials are
+// summed in split order (fp32), then the GEMM's epilogue.
+template <GemmEpi EPI>
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(Nf4GemmArgs a, int S) {
+    constexpr int NF = EPI == GemmEpi::kSwiGlu ? 2 : 1;
+    const int64_t quads = a.m * a.n / 4;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= quads) {
+        return;
+    }
+    const int64_t m = idx / (a.n / 4);
+    const int64_t nb = (idx % (a.n / 4)) * 4;
+    float v[NF][4];
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+        const float* src = a.partials + (static_cast<int64_t>(f) * S * a.m + m) * a.n + nb;
+        float4 acc = *reinterpret_cast<const float4*>(src);
+        for (int s = 1; s < S; ++s) {
+            const float4 p = *reinterpret_cast<const float4*>(src + static_cast<int64_t>(s) * a.m * a.n);
+            acc.x = acc.x + p.x;
+            acc.y = acc.y + p.y;
+            acc.z = acc.z + p.z;
+            acc.w = acc.w + p.w;
+        }
+        v[f][0] = acc.x;
+        v[f][1] = acc.y;
+        v[f][2] = acc.z;
+        v[f][3] = acc.w;
+    }
+    uint16_t h[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if constexpr (EPI == GemmEpi::kBias) {
+            h[i] = Bf16::store(a.bias != nullptr ? v[0][i] + Bf16::load(a.bias[nb + i]) : v[0][i]);
+        } else if constexpr (EPI == GemmEpi::kResidual) {
+            const float res = Bf16::load(a.residual[m * a.n + nb + i]);
+            h[i] = Bf16::store(res + Bf16::load(Bf16::store(v[0][i])));
+        } else {
+            h[i] = Bf16::store(silu_fixed(v[0][i]) * v[NF - 1][i]);
+        }
+    }
+    *reinterpret_cast<uint2*>(a.out + m * a.n + nb) =
+        make_uint2(static_cast<uint32_t>(h[0]) | (static_cast<uint32_t>(h[1]) << 16),
+                   static_cast<uint32_t>(h[2]) | (static_cast<uint32_t>(h[3]) << 16));
+}
+
+template <GemmEpi EPI>
+hipError_t launch_gemm_epi(const Nf4GemmArgs& a, hipStream_t stream) {
+    constexpr int NF = EPI == GemmEpi::kSwiGlu ? 2 : 1;
+    int64_t S = 1;
+    if (a.partials != nullptr) {
+        // ~1024 waves: one 16-row fragment per wave, K windows split over blocks
+        const int64_t row_waves = NF * a.n / kRowsPerWave;
+        const int64_t windows = a.k / kWindow;
+        S = (1024 + row_waves - 1) / row_waves;
+        S = S < windows ? S : windows;
+        S = S < 64 ? S : 64;
+        while (S > 1 && NF * S * a.m * a.n > a.partial_floats) {
+            --S;
+        }
+        if (S > 1) {
+            const int64_t per_split = (windows + S - 1) / S;
+            S = (windows + per_split - 1) / per_split;  // no empty split
+        }
+    }
+    const int64_t block_rows = EPI == GemmEpi::kSwiGlu ? kRowsPerBlock / 2 : kRowsPerBlock;
+    const dim3 grid(static_cast<unsigned>(a.n / block_rows), static_cast<unsigned>(S));
+    switch ((a.m + 15) / 16) {
+        case 1:
+            hipLaunchKernelGGL((nf4_gemm_kernel<EPI, 1>), grid, dim3(kGemmThreads), 0, stream, a);
+            break;
+        case 2:
+            hipLaunchKernelGGL((nf4_gemm_kernel<EPI, 2>), grid, dim3(kGemmThreads), 0, stream, a);
+            break;
+        case 3:
+            hipLaunchKernelGGL((nf4_gemm_kernel<EPI, 3>), grid, dim3(kGemmThreads), 0, stream, a);
+            break;
+        default:
+            hipLaunchKernelGGL((nf4_gemm_kernel<EPI, kTokenTiles>), grid, dim3(kGemmThreads), 0, stream, a);
+            break;
+    }
+    hipError_t status = hipGetLastError();
+    if (status != hipSuccess || S == 1) {
+        return status;
+    }
+    const int64_t quads = a.m * a.n / 4;
+    hipLaunchKernelGGL(gemm_reduce_kernel<EPI>, dim3(static_cast<unsigned>((quads + 255) / 256)), dim3(256), 0,
+                       stream, a, static_cast<int>(S));
+    return hipGetLastError();
 }
 
 }  // namespace
@@ -173,19 +334,15 @@ hipError_t launch_nf4_gemm(GemmEpi epi, const Nf4GemmArgs& a, hipStream_t stream
         (epi == GemmEpi::kResidual && a.residual == nullptr)) {
         return hipErrorInvalidValue;
     }
-    const dim3 grid(static_cast<unsigned>(a.n / kRowsPerBlock));
     switch (epi) {
         case GemmEpi::kBias:
-            hipLaunchKernelGGL(nf4_gemm_kernel<GemmEpi::kBias>, grid, dim3(kGemmThreads), 0, stream, a);
-            break;
+            return launch_gemm_epi<GemmEpi::kBias>(a, stream);
         case GemmEpi::kResidual:
-            hipLaunchKernelGGL(nf4_gemm_kernel<GemmEpi::kResidual>, grid, dim3(kGemmThreads), 0, stream, a);
-            break;
+            return launch_gemm_epi<GemmEpi::kResidual>(a, stream);
         case GemmEpi::kSwiGlu:
-            hipLaunchKernelGGL(nf4_gemm_kernel<GemmEpi::kSwiGlu>, grid, dim3(kGemmThreads), 0, stream, a);
-            break;
+            return launch_gemm_epi<GemmEpi::kSwiGlu>(a, stream);
     }
-    return hipGetLastError();
+    return hipErrorInvalidValue;
 }
 
 }  // namespace kc

@@ -54,6 +54,7 @@ struct Handle {
     // fixed scratch for the standalone attention / argmax entry points
     void* scratch = nullptr;
     float* gqa_partials = nullptr;
+    float* gemm_partials = nullptr;  // kc::kGemmScratchFloats (split-K of the prefill GEMMs)
     float* lm_best = nullptr;
     uint32_t* counters = nullptr;  // [0..1] attention, [2] lm_head
     int32_t* argmax_slot = nullptr;
@@ -457,8 +458,9 @@ hipError_t gemm_chunks(GemmEpi epi, Nf4GemmArgs a, int64_t tokens, hipStream_t s
 // norm + lm_head + argmax of the last row with the decode bookkeeping
 // (tokens[start+count] = argmax, step = start+count).  Workspace per token:
 // hidden, normalised x, q, k, v, attention output (bf16) and the SwiGLU
-// output (bf16 [11008]).
+// output (bf16 [11008]); then the GEMMs' split-K scratch.
 constexpr int64_t kPrefillBytesPerToken = (4 * 2048 + 2 * 256 + 11008) * 2;
+constexpr int64_t kPrefillFixedBytes = kGemmScratchFloats * 4;
 
 hipError_t model_prefill(const Model& m, uint8_t* ws, int64_t start, int64_t count, hipStream_t stream) {
     const auto& G = m.g;
@@ -469,6 +471,7 @@ hipError_t model_prefill(const Model& m, uint8_t* ws, int64_t start, int64_t cou
     uint16_t* v = k + count * 256;
     uint16_t* attn = v + count * 256;
     uint16_t* mlp = attn + count * 2048;
+    float* gemm_partials = reinterpret_cast<float*>(ws + count * kPrefillBytesPerToken);
     const float qk_scale_log2 = static_cast<float>(1.0 / std::sqrt(128.0)) * kLog2e;
     hipError_t st = hipSuccess;
     auto gemm = [&](GemmEpi epi, const uint16_t* x, uint64_t w0, uint64_t a0, uint64_t w1, uint64_t a1,
@@ -484,6 +487,8 @@ hipError_t model_prefill(const Model& m, uint8_t* ws, int64_t start, int64_t cou
         a.out = out;
         a.n = n;
         a.k = kdim;
+        a.partials = gemm_partials;
+        a.partial_floats = kGemmScratchFloats;
         return gemm_chunks(epi, a, count, stream);
     };
     for (int64_t layer = 0; layer < m.num_layers && st == hipSuccess; ++layer) {
@@ -623,7 +628,8 @@ void* kudacuda_create(int device_id) {
     const size_t partial_bytes = static_cast<size_t>(kc::gqa_workspace(kc::kMaxStandaloneKv)) * sizeof(float);
     const size_t best_bytes = static_cast<size_t>(kc::lm_head_workspace_floats()) * sizeof(float);
     const size_t counter_bytes = 64;
-    const size_t total = partial_bytes + best_bytes + counter_bytes;
+    const size_t gemm_bytes = static_cast<size_t>(kc::kGemmScratchFloats) * sizeof(float);
+    const size_t total = partial_bytes + best_bytes + counter_bytes + gemm_bytes;
     status = hipMalloc(&h->scratch, total);
     if (status != hipSuccess) {
         h->scratch = nullptr;
@@ -635,6 +641,7 @@ void* kudacuda_create(int device_id) {
     h->lm_best = reinterpret_cast<float*>(base + partial_bytes);
     h->counters = reinterpret_cast<uint32_t*>(base + partial_bytes + best_bytes);
     h->argmax_slot = reinterpret_cast<int32_t*>(base + partial_bytes + best_bytes + 32);
+    h->gemm_partials = reinterpret_cast<float*>(base + partial_bytes + best_bytes + counter_bytes);
     status = hipMemset(h->counters, 0, counter_bytes);
     if (status == hipSuccess) {
         status = hipDeviceSynchronize();
@@ -961,6 +968,8 @@ int kudacuda_nf4_gemm_bf16(void* raw, uint64_t input, uint64_t weight_packed, ui
     a.out = ptr<uint16_t>(output);
     a.n = out_features;
     a.k = in_features;
+    a.partials = h->gemm_partials;
+    a.partial_floats = kc::kGemmScratchFloats;
     const kc::GemmEpi epi = residual != 0 ? kc::GemmEpi::kResidual : kc::GemmEpi::kBias;
     return finish(h, symbol, kc::gemm_chunks(epi, a, tokens, as_stream(stream)));
 }
@@ -990,6 +999,8 @@ int kudacuda_nf4_gemm_swiglu_bf16(void* raw, uint64_t input, uint64_t gate_weigh
     a.out = ptr<uint16_t>(output);
     a.n = out_features;
     a.k = in_features;
+    a.partials = h->gemm_partials;
+    a.partial_floats = kc::kGemmScratchFloats;
     return finish(h, symbol, kc::gemm_chunks(kc::GemmEpi::kSwiGlu, a, tokens, as_stream(stream)));
 }
 
@@ -1318,7 +1329,7 @@ int kudacuda_qwen2_model_step(void* raw_model, uint64_t stream) {
 }
 
 int64_t kudacuda_qwen2_prefill_workspace_bytes(int64_t tokens) {
-    return tokens < 1 ? 0 : tokens * kc::kPrefillBytesPerToken;
+    return tokens < 1 ? 0 : tokens * kc::kPrefillBytesPerToken + kc::kPrefillFixedBytes;
 }
 
 int kudacuda_qwen2_model_prefill(void* raw_model, uint64_t workspace, int64_t workspace_bytes, int64_t start,

@@ -1,6 +1,7 @@
-"""Per-op throughput of the decode kernels at the BASELINE op configs (1-4).
+"""Per-op throughput of the decode kernels at the BASELINE op configs (1-4),
+and of the prefill NF4 GEMMs at 64 tokens (6).
 
-    python -m kudacuda_amd.opbench [--configs 1 2 3 4] [--launches 256]
+    python -m kudacuda_amd.opbench [--configs 1 2 3 4 6] [--launches 256]
 
 Each measurement captures ``launches`` back-to-back calls of one C-ABI entry
 point into a hipGraph (so host launch cost is excluded), cycling through
@@ -140,6 +141,36 @@ class Bench:
         self.report("mlp_nf4_gate_up_down", 3, self.time(launch_mlp), nbytes, copies=n)
         self.report("swiglu_nf4_gate_up", 3, self.time(launch_swiglu), gate_up, copies=n)
 
+    def prefill_gemm(self) -> None:
+        """NF4 GEMMs of the multi-token prefill at M = 64 tokens (MFMA): bytes =
+        NF4 weights + absmax + bf16 activations in and out; flops = 2 M N K."""
+
+        m = 64
+        s = self.stream.cuda_stream
+        cases = (("q_proj", 2048, 2048, False), ("gate_up_swiglu", 11008, 2048, True), ("down", 2048, 11008, False))
+        for name, n, k, swiglu in cases:
+            nw = 2 if swiglu else 1
+            nbytes = nw * _nf4_bytes(n, k) + 2 * m * k + 2 * m * n
+            copies = self.copies_for(nbytes)
+            ws = [[(self.rand_u8(n * k // 2), self.absmax(n * k // 64)) for _ in range(nw)] for _ in range(copies)]
+            x, y = self.rand_bf16(m * k), self.rand_bf16(m * n)
+
+            def launch(i: int, ws=ws, x=x, y=y, n=n, k=k, swiglu=swiglu) -> None:
+                w = ws[i % len(ws)]
+                if swiglu:
+                    self.native.call("kudacuda_nf4_gemm_swiglu_bf16", x.data_ptr(), w[0][0].data_ptr(),
+                                     w[0][1].data_ptr(), w[1][0].data_ptr(), w[1][1].data_ptr(), y.data_ptr(), m, k,
+                                     n, 64, s)
+                else:
+                    self.native.call("kudacuda_nf4_gemm_bf16", x.data_ptr(), w[0][0].data_ptr(), w[0][1].data_ptr(),
+                                     0, 0, y.data_ptr(), m, k, n, 64, s)
+
+            us = self.time(launch)
+            self.report(f"prefill_gemm_{name}", 6, us, nbytes, tokens=m, copies=copies,
+                        tflops=round(2.0 * m * n * k * nw / (us * 1e-6) / 1e12, 2))
+            del ws
+            self.torch.cuda.empty_cache()
+
     def gqa(self) -> None:
         s = self.stream.cuda_stream
         scale = 1.0 / math.sqrt(128.0)
@@ -161,7 +192,7 @@ class Bench:
 
 def main(argv: list[str] | None = None) -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    parser.add_argument("--configs", type=int, nargs="+", default=[1, 2, 3, 4])
+    parser.add_argument("--configs", type=int, nargs="+", default=[1, 2, 3, 4, 6])
     parser.add_argument("--launches", type=int, default=256)
     parser.add_argument("--copy-mib", type=int, default=0,
                         help="first run 3 plain device copies of this many MiB (counter calibration)")
@@ -181,7 +212,7 @@ def main(argv: list[str] | None = None) -> int:
                   flush=True)
             del src, dst
         for config in args.configs:
-            {1: bench.gemv, 2: bench.qkv, 3: bench.mlp, 4: bench.gqa}[config]()
+            {1: bench.gemv, 2: bench.qkv, 3: bench.mlp, 4: bench.gqa, 6: bench.prefill_gemm}[config]()
     bench.native.close()
     return 0
 

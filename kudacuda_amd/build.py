@@ -41,6 +41,14 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-source additions.  kc_prefill.hip: MFMA accumulators in VGPRs (the
+# default AGPR form makes the compiler shuffle accumulators between register
+# files inside the GEMM's window loop).
+SOURCE_FLAGS = {
+    "kc_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _hipcc() -> str:
     for candidate in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if candidate and Path(candidate).exists():
@@ -73,7 +81,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
 
     def compile_one(pair: tuple[Path, Path]) -> None:
         source, obj = pair
-        command = [hipcc, *HIPCC_FLAGS, "-c", str(source), "-o", str(obj)]
+        command = [hipcc, *HIPCC_FLAGS, *SOURCE_FLAGS.get(source.name, []), "-c", str(source), "-o", str(obj)]
         if verbose:
             print(" ".join(command))
         _run(command)

@@ -56,54 +56,100 @@ __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast
 // 8 codes of one 32-bit word (byte b: element 2b in the high nibble, 2b+1 in
 // the low nibble) times absmax, each rounded to bf16 (round to nearest even,
 // v_cvt_pk_bf16_f32; the products are finite); element j lands in slot j.
+// The codebook byte offsets (4 * code) come from two shifted copies of the
+// word: byte b of (word >> 2) holds the high nibble of byte b at bits 2..5,
+// byte b of (word << 2) the low nibble, so each offset is one byte-select AND.
+// (written as asm: the compiler folds a byte-select AND back into a shift and
+// an AND).
+template <int B>
+__device__ __forceinline__ uint32_t byte_and_3c(uint32_t x) {
+    uint32_t r;
+    if constexpr (B == 0) {
+        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
+            : "=v"(r) : "v"(0x3cu), "v"(x));
+    } else if constexpr (B == 1) {
+        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1"
+            : "=v"(r) : "v"(0x3cu), "v"(x));
+    } else if constexpr (B == 2) {
+        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2"
+            : "=v"(r) : "v"(0x3cu), "v"(x));
+    } else {
+        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3"
+            : "=v"(r) : "v"(0x3cu), "v"(x));
+    }
+    return r;
+}
+
+template <int B>
+__device__ __forceinline__ void dequant_byte(bf16x8& v, uint32_t hi4, uint32_t lo4, float am, const char* base) {
+    const uint32_t oh = byte_and_3c<B>(hi4);
+    const uint32_t ol = byte_and_3c<B>(lo4);
+    v[2 * B] = static_cast<__bf16>(*reinterpret_cast<const float*>(base + oh) * am);
+    v[2 * B + 1] = static_cast<__bf16>(*reinterpret_cast<const float*>(base + ol) * am);
+}
+
 __device__ __forceinline__ bf16x8 dequant8_bf16(uint32_t word, float am, const float* cb) {
+    const uint32_t hi4 = word >> 2;
+    const uint32_t lo4 = word << 2;
+    const char* base = reinterpret_cast<const char*>(cb);
     bf16x8 v;
+    dequant_byte<0>(v, hi4, lo4, am, base);
+    dequant_byte<1>(v, hi4, lo4, am, base);
+    dequant_byte<2>(v, hi4, lo4, am, base);
+    dequant_byte<3>(v, hi4, lo4, am, base);
+    return v;
+}
+
+// One window's x requests of a thread, kept as one vector value (slots
+// 4j..4j+3: its 16-byte piece of token row 16j + tid/16, bytes 16 (tid%16)
+// of the row's window slice), and one window's weight requests of a lane
+// (slots 0..3: 32 codes of its row, slot 4: their absmax bits).  Plain
+// vector values stay in registers through the rotation below.
+typedef uint32_t u32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
+
+template <int NT>
+__device__ __forceinline__ u32x16 x_fetch(const uint16_t* const* xrow, int xcol, int64_t kw) {
+    u32x16 v = {};
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-        const uint32_t byte = (word >> (8 * b)) & 0xffu;
-        v[2 * b] = static_cast<__bf16>(cb[byte >> 4] * am);
-        v[2 * b + 1] = static_cast<__bf16>(cb[byte & 0xfu] * am);
+    for (int j = 0; j < NT; ++j) {
+        const uint4 t = *reinterpret_cast<const uint4*>(xrow[j] + kw + xcol);
+        v[4 * j] = t.x;
+        v[4 * j + 1] = t.y;
+        v[4 * j + 2] = t.z;
+        v[4 * j + 3] = t.w;
     }
     return v;
 }
 
-// One window's requests of a thread: its NT 16-byte pieces of the x tile
-// (token row 16j + tid/16, bytes 16 (tid%16) of the row's window slice) and
-// its wave's weight codes (32 per lane) with their absmax.
-template <int NT>
-struct GemmFetch {
-    uint4 x[NT];
-    uint4 w;
-    float am;
-};
-
-template <int NT>
-__device__ __forceinline__ void gemm_fetch(GemmFetch<NT>& o, const uint16_t* const* xrow, int xcol,
-                                           const uint8_t* wrow, const float* arow, int64_t kw, int q) {
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-        o.x[j] = *reinterpret_cast<const uint4*>(xrow[j] + kw + xcol);
-    }
+__device__ __forceinline__ u32x8 w_fetch(const uint8_t* wrow, const float* arow, int64_t kw, int q) {
     const int64_t kq = kw + 32 * q;
-    o.w = *reinterpret_cast<const uint4*>(wrow + kq / 2);
-    o.am = arow[kq / 64];
+    const uint4 t = *reinterpret_cast<const uint4*>(wrow + kq / 2);
+    u32x8 v = {};
+    v[0] = t.x;
+    v[1] = t.y;
+    v[2] = t.z;
+    v[3] = t.w;
+    v[4] = __float_as_uint(arow[kq / 64]);
+    return v;
 }
 
 template <int NT>
-__device__ __forceinline__ void gemm_stage(uint8_t* buf, const GemmFetch<NT>& o, int tid) {
+__device__ __forceinline__ void x_stage(uint8_t* buf, const u32x16& o, int tid) {
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
-        *reinterpret_cast<uint4*>(buf + (16 * j + tid / 16) * kXPitch + 16 * (tid % 16)) = o.x[j];
+        *reinterpret_cast<uint4*>(buf + (16 * j + tid / 16) * kXPitch + 16 * (tid % 16)) =
+            make_uint4(o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]);
     }
 }
 
 template <int NT>
-__device__ __forceinline__ void gemm_window(const uint8_t* buf, const GemmFetch<NT>& o, floatx4* acc, int r, int q,
+__device__ __forceinline__ void gemm_window(const uint8_t* buf, const u32x8& o, floatx4* acc, int r, int q,
                                             const float* cb) {
+    const float am = __uint_as_float(o[4]);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-        const uint32_t word = s == 0 ? o.w.x : (s == 1 ? o.w.y : (s == 2 ? o.w.z : o.w.w));
-        const bf16x8 A = dequant8_bf16(word, o.am, cb);
+        const bf16x8 A = dequant8_bf16(o[s], am, cb);
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const uint4 B = *reinterpret_cast<const uint4*>(buf + (16 * t + r) * kXPitch + 64 * q + 16 * s);
@@ -150,22 +196,45 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(Nf4GemmArgs a) {
     for (int t = 0; t < NT; ++t) {
         acc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     }
-    GemmFetch<NT> cur, nxt;
-    gemm_fetch<NT>(cur, xrow, xcol, wrow, arow, k_begin, q);
-    gemm_stage<NT>(s_x[0], cur, tid);
+    // x and weights are requested two windows ahead into three register
+    // slots that rotate through the unrolled loop; x of window w + 1 is
+    // staged into the other LDS buffer while window w is computed, and only
+    // waits for requests older than the ones just issued.  Requests past the
+    // split's last window are clamped to a window of the split, never used.
+    constexpr int kBuf = 16 * NT * kXPitch;
+    uint8_t* const sx = &s_x[0][0];
+    const int64_t k1 = k_begin + kWindow < k_end ? k_begin + kWindow : k_begin;
+    u32x16 x0 = x_fetch<NT>(xrow, xcol, k_begin);
+    u32x8 w0 = w_fetch(wrow, arow, k_begin, q);
+    u32x16 x1 = x_fetch<NT>(xrow, xcol, k1);
+    u32x8 w1 = w_fetch(wrow, arow, k1, q);
+    u32x16 x2;
+    u32x8 w2;
+    x_stage<NT>(sx, x0, tid);
     __syncthreads();
     int buf = 0;
-    for (int64_t kw = k_begin; kw < k_end; kw += kWindow) {
-        // the split's last window is requested again and staged unused
-        const int64_t kn = kw + kWindow < k_end ? kw + kWindow : kw;
-        gemm_fetch<NT>(nxt, xrow, xcol, wrow, arow, kn, q);
-        __builtin_amdgcn_sched_barrier(0);  // keep the requests ahead of the compute
-        gemm_window<NT>(s_x[buf], cur, acc, r, q, cb);
-        gemm_stage<NT>(s_x[buf ^ 1], nxt, tid);
-        __syncthreads();
-        cur = nxt;
-        buf ^= 1;
+    int64_t kw = k_begin;
+#define KC_GEMM_STEP(XF, WF, WC, XS)                                               \
+    {                                                                              \
+        const int64_t kf = kw + 2 * kWindow < k_end ? kw + 2 * kWindow : kw;       \
+        XF = x_fetch<NT>(xrow, xcol, kf);                                          \
+        WF = w_fetch(wrow, arow, kf, q);                                           \
+        __builtin_amdgcn_sched_barrier(0); /* requests ahead of the compute */     \
+        gemm_window<NT>(sx + buf * kBuf, WC, acc, r, q, cb);                      \
+        x_stage<NT>(sx + (buf ^ 1) * kBuf, XS, tid);                               \
+        __syncthreads();                                                           \
+        buf ^= 1;                                                                  \
+        kw += kWindow;                                                             \
+        if (kw >= k_end) {                                                         \
+            break;                                                                 \
+        }                                                                          \
     }
+    while (true) {
+        KC_GEMM_STEP(x2, w2, w0, x1)
+        KC_GEMM_STEP(x0, w0, w1, x2)
+        KC_GEMM_STEP(x1, w1, w2, x0)
+    }
+#undef KC_GEMM_STEP
 
     // D[4q + i][r]: rows n0w + 4q + i, token 16t + r; four consecutive rows
     // per lane go out as one store

@@ -98,25 +98,41 @@ hipError_t launch_nf4_down11008(Act act, const Nf4DownArgs& args, hipStream_t st
 // x bf16 [m, k] row-major, weights in the bitsandbytes layout ([n, k/2] codes,
 // [n, k/64] fp32 absmax), fp32 accumulation.  m <= kGemmMaxTokens per launch,
 // n % 64 == 0, k % 128 == 0.
-enum class GemmEpi { kBias = 0, kResidual = 1, kSwiGlu = 2 };
+enum class GemmEpi { kBias = 0, kResidual = 1, kSwiGlu = 2, kQkvRope = 3 };
 constexpr int kGemmMaxTokens = 64;
 // split-K scratch: fp32 partial tiles [weights][splits][m][n]
 constexpr int64_t kGemmScratchFloats = int64_t{4} << 20;
 struct Nf4GemmArgs {
     const uint16_t* x = nullptr;
-    const uint8_t* w[2] = {nullptr, nullptr};       // kSwiGlu: gate, up
-    const float* absmax[2] = {nullptr, nullptr};
+    const uint8_t* w[3] = {nullptr, nullptr, nullptr};  // kSwiGlu: gate, up; kQkvRope: q, k, v
+    const float* absmax[3] = {nullptr, nullptr, nullptr};
     const uint16_t* bias = nullptr;      // kBias: [n] (may be null: no bias)
     const uint16_t* residual = nullptr;  // kResidual: [m, n], may alias out
-    uint16_t* out = nullptr;             // [m, n]
+    uint16_t* out = nullptr;             // [m, n]; kQkvRope: rotated q [m, q_rows]
     int64_t m = 0;
-    int64_t n = 0;
+    int64_t n = 0;  // kQkvRope: q_rows + 2 kv_rows
     int64_t k = 0;
     // Split-K scratch (null: one block column per row tile).  With it, K is
     // split so the launch has ~1024 waves; partial tiles are summed in split
-    // order by a second kernel that applies the epilogue.
+    // order by a second kernel that applies the epilogue.  kQkvRope always
+    // splits (its epilogue lives in that second kernel).
     float* partials = nullptr;
     int64_t partial_floats = 0;
+    // kQkvRope: rows [0, q_rows) of the output come from w[0], the next
+    // kv_rows from w[1], the last kv_rows from w[2] (head dim 128, each a
+    // multiple of 64); biases per segment; the epilogue adds the bias
+    // (bf16 rounding), rotates q and k by RoPE at position start + row
+    // (cos/sin tables [position][64]) and writes k and v rows into the caches
+    // [kv heads, capacity, 128].
+    int64_t q_rows = 0;
+    int64_t kv_rows = 0;
+    const uint16_t* seg_bias[3] = {nullptr, nullptr, nullptr};
+    const float* rope_cos = nullptr;
+    const float* rope_sin = nullptr;
+    uint16_t* kcache = nullptr;
+    uint16_t* vcache = nullptr;
+    int64_t capacity = 0;
+    int64_t start = 0;
 };
 hipError_t launch_nf4_gemm(GemmEpi epi, const Nf4GemmArgs& args, hipStream_t stream);
 
@@ -137,23 +153,6 @@ struct PrefillNormArgs {
     int64_t m = 0;
 };
 hipError_t launch_prefill_norm(const PrefillNormArgs& args, hipStream_t stream);
-
-// RoPE on q [m, 16, 128] (in place) and k [m, 2, 128] at positions start + r
-// (pairs (d, d + 64), tables [capacity, 64]); k and v rows go to the caches
-// [2, capacity, 128] at those positions.
-struct PrefillRopeArgs {
-    uint16_t* q = nullptr;
-    const uint16_t* k = nullptr;
-    const uint16_t* v = nullptr;
-    const float* rope_cos = nullptr;
-    const float* rope_sin = nullptr;
-    uint16_t* kcache = nullptr;
-    uint16_t* vcache = nullptr;
-    int64_t capacity = 0;
-    int64_t start = 0;
-    int64_t m = 0;
-};
-hipError_t launch_prefill_rope_cache(const PrefillRopeArgs& args, hipStream_t stream);
 
 // Causal GQA attention of m query rows (positions start + r) over cache rows
 // [0, start + r]: out [m, 2048] bf16.

@@ -176,11 +176,19 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(Nf4GemmArgs a) {
     const int64_t per_split = (windows + S - 1) / S;
     const int64_t k_begin = static_cast<int64_t>(blockIdx.y) * per_split * kWindow;
     const int64_t k_end = k_begin + per_split * kWindow < K ? k_begin + per_split * kWindow : K;
-    // this wave's fragment: f = 0 (gate or plain) / 1 (up), first row n0w
+    // this wave's fragment: f = 0 (gate or plain) / 1 (up), first output
+    // column n0w; kQkvRope: the block's 64 rows lie in the q, k or v weight
+    // (segment boundaries are multiples of 64), row0 is the row in it
     const int f = kSw ? wave >> 1 : 0;
     const int64_t n0w = static_cast<int64_t>(blockIdx.x) * kBlockRows + (kSw ? wave & 1 : wave) * kRowsPerWave;
-    const uint8_t* wrow = a.w[f] + (n0w + r) * (K / 2);  // n % 64 == 0: every row exists
-    const float* arow = a.absmax[f] + (n0w + r) * (K / 64);
+    int seg = f;
+    int64_t row0 = n0w;
+    if constexpr (EPI == GemmEpi::kQkvRope) {
+        seg = n0w < a.q_rows ? 0 : (n0w < a.q_rows + a.kv_rows ? 1 : 2);
+        row0 = n0w - (seg == 0 ? 0 : (seg == 1 ? a.q_rows : a.q_rows + a.kv_rows));
+    }
+    const uint8_t* wrow = a.w[seg] + (row0 + r) * (K / 2);  // every row exists (multiples of 64)
+    const float* arow = a.absmax[seg] + (row0 + r) * (K / 64);
     // x rows this thread stages (rows past m re-read row m - 1; never used)
     const uint16_t* xrow[NT];
 #pragma unroll
@@ -248,6 +256,9 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(Nf4GemmArgs a) {
             }
         }
         return;
+    }
+    if constexpr (EPI == GemmEpi::kQkvRope) {
+        return;  // always split: the epilogue is in qkv_rope_reduce_kernel
     }
     floatx4 up[NT];
     if constexpr (kSw) {
@@ -349,11 +360,89 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(Nf4GemmArgs a, int S) 
                    static_cast<uint32_t>(h[2]) | (static_cast<uint32_t>(h[3]) << 16));
 }
 
+// kQkvRope epilogue.  Per token, thread u handles (d, d + 1) and their RoPE
+// partners (d + 64, d + 65) of one q head (u < q_rows / 4) or k head (next
+// kv_rows / 4), or 4 consecutive v values (last kv_rows / 4): split partials
+// summed in split order, bias added in fp32 and the sum rounded to bf16 (the
+// plain kBias epilogue), then the rotation in fp32 from the bf16 values,
+// rounded again.  Rotated q goes to out [m, q_rows], rotated k and v to the
+// caches at position start + row.
+__global__ __launch_bounds__(256) void qkv_rope_reduce_kernel(Nf4GemmArgs a, int S) {
+    const int64_t per_row = (a.q_rows + 2 * a.kv_rows) / 4;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= a.m * per_row) {
+        return;
+    }
+    const int64_t m = idx / per_row;
+    const int64_t u = idx % per_row;
+    const int64_t pos = a.start + m;
+    const int64_t q_units = a.q_rows / 4;
+    const int64_t k_units = a.kv_rows / 4;
+    const float* src = a.partials + m * a.n;
+    const int64_t plane = a.m * a.n;
+    if (u >= q_units + k_units) {
+        const int64_t c = a.q_rows + a.kv_rows + 4 * (u - q_units - k_units);  // v column
+        float4 acc = *reinterpret_cast<const float4*>(src + c);
+        for (int s = 1; s < S; ++s) {
+            const float4 p = *reinterpret_cast<const float4*>(src + s * plane + c);
+            acc.x = acc.x + p.x;
+            acc.y = acc.y + p.y;
+            acc.z = acc.z + p.z;
+            acc.w = acc.w + p.w;
+        }
+        const int64_t cv = c - a.q_rows - a.kv_rows;
+        const uint16_t* b = a.seg_bias[2];
+        const float vs[4] = {acc.x, acc.y, acc.z, acc.w};
+        uint16_t h[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            h[i] = Bf16::store(b != nullptr ? vs[i] + Bf16::load(b[cv + i]) : vs[i]);
+        }
+        uint16_t* dst = a.vcache + ((cv / 128) * a.capacity + pos) * 128 + cv % 128;
+        *reinterpret_cast<uint2*>(dst) = make_uint2(static_cast<uint32_t>(h[0]) | (static_cast<uint32_t>(h[1]) << 16),
+                                                    static_cast<uint32_t>(h[2]) | (static_cast<uint32_t>(h[3]) << 16));
+        return;
+    }
+    const bool is_q = u < q_units;
+    const int64_t uu = is_q ? u : u - q_units;
+    const int64_t head = uu / 32;
+    const int d = static_cast<int>(uu % 32) * 2;
+    const int64_t c0 = (is_q ? 0 : a.q_rows) + head * 128 + d;  // partial column of (d, d + 1)
+    float2 lo = *reinterpret_cast<const float2*>(src + c0);
+    float2 hi = *reinterpret_cast<const float2*>(src + c0 + 64);
+    for (int s = 1; s < S; ++s) {
+        const float2 pl = *reinterpret_cast<const float2*>(src + s * plane + c0);
+        const float2 ph = *reinterpret_cast<const float2*>(src + s * plane + c0 + 64);
+        lo.x = lo.x + pl.x;
+        lo.y = lo.y + pl.y;
+        hi.x = hi.x + ph.x;
+        hi.y = hi.y + ph.y;
+    }
+    const uint16_t* b = is_q ? a.seg_bias[0] : a.seg_bias[1];
+    const int64_t cb0 = head * 128 + d;  // column within the segment
+    const float l0 = Bf16::load(Bf16::store(b != nullptr ? lo.x + Bf16::load(b[cb0]) : lo.x));
+    const float l1 = Bf16::load(Bf16::store(b != nullptr ? lo.y + Bf16::load(b[cb0 + 1]) : lo.y));
+    const float h0 = Bf16::load(Bf16::store(b != nullptr ? hi.x + Bf16::load(b[cb0 + 64]) : hi.x));
+    const float h1 = Bf16::load(Bf16::store(b != nullptr ? hi.y + Bf16::load(b[cb0 + 65]) : hi.y));
+    const float c_0 = a.rope_cos[pos * 64 + d];
+    const float c_1 = a.rope_cos[pos * 64 + d + 1];
+    const float s_0 = a.rope_sin[pos * 64 + d];
+    const float s_1 = a.rope_sin[pos * 64 + d + 1];
+    const uint32_t rl = static_cast<uint32_t>(Bf16::store((l0 * c_0) - (h0 * s_0))) |
+                        (static_cast<uint32_t>(Bf16::store((l1 * c_1) - (h1 * s_1))) << 16);
+    const uint32_t rh = static_cast<uint32_t>(Bf16::store((h0 * c_0) + (l0 * s_0))) |
+                        (static_cast<uint32_t>(Bf16::store((h1 * c_1) + (l1 * s_1))) << 16);
+    uint16_t* dst = is_q ? a.out + m * a.q_rows + head * 128 + d : a.kcache + (head * a.capacity + pos) * 128 + d;
+    *reinterpret_cast<uint32_t*>(dst) = rl;
+    *reinterpret_cast<uint32_t*>(dst + 64) = rh;
+}
+
 template <GemmEpi EPI>
 hipError_t launch_gemm_epi(const Nf4GemmArgs& a, hipStream_t stream) {
     constexpr int NF = EPI == GemmEpi::kSwiGlu ? 2 : 1;
     int64_t S = 1;
     if (a.partials != nullptr) {
+        // (kQkvRope: at least 2, its epilogue is the split reduce)
         // ~1024 waves: one 16-row fragment per wave, K windows split over blocks
         const int64_t row_waves = NF * a.n / kRowsPerWave;
         const int64_t windows = a.k / kWindow;
@@ -362,6 +451,9 @@ hipError_t launch_gemm_epi(const Nf4GemmArgs& a, hipStream_t stream) {
         S = S < 64 ? S : 64;
         while (S > 1 && NF * S * a.m * a.n > a.partial_floats) {
             --S;
+        }
+        if (EPI == GemmEpi::kQkvRope && S < 2) {
+            S = 2;
         }
         if (S > 1) {
             const int64_t per_split = (windows + S - 1) / S;
@@ -389,8 +481,13 @@ hipError_t launch_gemm_epi(const Nf4GemmArgs& a, hipStream_t stream) {
         return status;
     }
     const int64_t quads = a.m * a.n / 4;
-    hipLaunchKernelGGL(gemm_reduce_kernel<EPI>, dim3(static_cast<unsigned>((quads + 255) / 256)), dim3(256), 0,
-                       stream, a, static_cast<int>(S));
+    if constexpr (EPI == GemmEpi::kQkvRope) {
+        hipLaunchKernelGGL(qkv_rope_reduce_kernel, dim3(static_cast<unsigned>((quads + 255) / 256)), dim3(256), 0,
+                           stream, a, static_cast<int>(S));
+    } else {
+        hipLaunchKernelGGL(gemm_reduce_kernel<EPI>, dim3(static_cast<unsigned>((quads + 255) / 256)), dim3(256), 0,
+                           stream, a, static_cast<int>(S));
+    }
     return hipGetLastError();
 }
 
@@ -403,6 +500,14 @@ hipError_t launch_nf4_gemm(GemmEpi epi, const Nf4GemmArgs& a, hipStream_t stream
         (epi == GemmEpi::kResidual && a.residual == nullptr)) {
         return hipErrorInvalidValue;
     }
+    if (epi == GemmEpi::kQkvRope &&
+        (a.partials == nullptr || a.q_rows < 128 || a.q_rows % 128 != 0 || a.kv_rows < 128 || a.kv_rows % 128 != 0 ||
+         a.n != a.q_rows + 2 * a.kv_rows || a.w[1] == nullptr || a.w[2] == nullptr || a.absmax[1] == nullptr ||
+         a.absmax[2] == nullptr || a.rope_cos == nullptr || a.rope_sin == nullptr || a.kcache == nullptr ||
+         a.vcache == nullptr || a.start < 0 || a.start + a.m > a.capacity ||
+         2 * a.m * a.n > a.partial_floats)) {
+        return hipErrorInvalidValue;
+    }
     switch (epi) {
         case GemmEpi::kBias:
             return launch_gemm_epi<GemmEpi::kBias>(a, stream);
@@ -410,6 +515,8 @@ hipError_t launch_nf4_gemm(GemmEpi epi, const Nf4GemmArgs& a, hipStream_t stream
             return launch_gemm_epi<GemmEpi::kResidual>(a, stream);
         case GemmEpi::kSwiGlu:
             return launch_gemm_epi<GemmEpi::kSwiGlu>(a, stream);
+        case GemmEpi::kQkvRope:
+            return launch_gemm_epi<GemmEpi::kQkvRope>(a, stream);
     }
     return hipErrorInvalidValue;
 }
@@ -417,7 +524,7 @@ hipError_t launch_nf4_gemm(GemmEpi epi, const Nf4GemmArgs& a, hipStream_t stream
 }  // namespace kc
 
 // ---------------------------------------------------------------------------
-// Row norm, RoPE + cache write and causal attention of the prefill.
+// Row norm and causal attention of the prefill.
 namespace kc {
 namespace {
 
@@ -476,45 +583,6 @@ __global__ __launch_bounds__(256) void prefill_norm_kernel(PrefillNormArgs a) {
 
 // grid m: thread t rotates the q pairs t, t+256, t+512, t+768 (head p/64,
 // dim p%64), k pair t (< 128) and copies k/v element t (< 256) to the caches.
-__global__ __launch_bounds__(256) void prefill_rope_cache_kernel(PrefillRopeArgs a) {
-    const int64_t row = blockIdx.x;
-    const int64_t pos = a.start + row;
-    const int t = threadIdx.x;
-    const float* cs = a.rope_cos + pos * 64;
-    const float* sn = a.rope_sin + pos * 64;
-    uint16_t* q = a.q + row * 2048;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int pair = t + 256 * i;
-        const int h = pair >> 6;
-        const int d = pair & 63;
-        const float c = cs[d];
-        const float s = sn[d];
-        const float v0 = Bf16::load(q[h * 128 + d]);
-        const float v1 = Bf16::load(q[h * 128 + d + 64]);
-        q[h * 128 + d] = Bf16::store((v0 * c) - (v1 * s));
-        q[h * 128 + d + 64] = Bf16::store((v1 * c) + (v0 * s));
-    }
-    const uint16_t* k = a.k + row * 256;
-    const uint16_t* v = a.v + row * 256;
-    if (t < 128) {
-        const int g = t >> 6;
-        const int d = t & 63;
-        const float c = cs[d];
-        const float s = sn[d];
-        const float v0 = Bf16::load(k[g * 128 + d]);
-        const float v1 = Bf16::load(k[g * 128 + d + 64]);
-        uint16_t* kc = a.kcache + (g * a.capacity + pos) * 128;
-        kc[d] = Bf16::store((v0 * c) - (v1 * s));
-        kc[d + 64] = Bf16::store((v1 * c) + (v0 * s));
-    }
-    {
-        const int g = t >> 7;
-        const int d = t & 127;
-        a.vcache[(g * a.capacity + pos) * 128 + d] = v[t];
-    }
-}
-
 constexpr int kAttnGroups = 32;  // 16-lane groups of a 512-thread block
 constexpr int kAttnHeads = 8;
 constexpr int kAttnDim = 128;
@@ -646,16 +714,6 @@ hipError_t launch_prefill_norm(const PrefillNormArgs& a, hipStream_t stream) {
     }
     const unsigned blocks = static_cast<unsigned>((a.m + kNormRowsPerBlock - 1) / kNormRowsPerBlock);
     hipLaunchKernelGGL(prefill_norm_kernel, dim3(blocks), dim3(256), 0, stream, a);
-    return hipGetLastError();
-}
-
-hipError_t launch_prefill_rope_cache(const PrefillRopeArgs& a, hipStream_t stream) {
-    if (a.m < 1 || a.start < 0 || a.start + a.m > a.capacity || a.q == nullptr || a.k == nullptr ||
-        a.v == nullptr || a.kcache == nullptr || a.vcache == nullptr || a.rope_cos == nullptr ||
-        a.rope_sin == nullptr) {
-        return hipErrorInvalidValue;
-    }
-    hipLaunchKernelGGL(prefill_rope_cache_kernel, dim3(static_cast<unsigned>(a.m)), dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 

@@ -440,11 +440,14 @@ hipError_t gemm_chunks(GemmEpi epi, Nf4GemmArgs a, int64_t tokens, hipStream_t s
     const uint16_t* x = a.x;
     const uint16_t* res = a.residual;
     uint16_t* out = a.out;
+    const int64_t start = a.start;
+    const int64_t out_stride = epi == GemmEpi::kQkvRope ? a.q_rows : a.n;
     for (int64_t m0 = 0; m0 < tokens; m0 += kGemmMaxTokens) {
         a.m = tokens - m0 < kGemmMaxTokens ? tokens - m0 : kGemmMaxTokens;
         a.x = x + m0 * a.k;
         a.residual = res != nullptr ? res + m0 * a.n : nullptr;
-        a.out = out + m0 * a.n;
+        a.out = out + m0 * out_stride;
+        a.start = start + m0;
         const hipError_t status = launch_nf4_gemm(epi, a, stream);
         if (status != hipSuccess) {
             return status;
@@ -457,9 +460,10 @@ hipError_t gemm_chunks(GemmEpi epi, Nf4GemmArgs a, int64_t tokens, hipStream_t s
 // from the device token array) through every layer at once, then the final
 // norm + lm_head + argmax of the last row with the decode bookkeeping
 // (tokens[start+count] = argmax, step = start+count).  Workspace per token:
-// hidden, normalised x, q, k, v, attention output (bf16) and the SwiGLU
-// output (bf16 [11008]); then the GEMMs' split-K scratch.
-constexpr int64_t kPrefillBytesPerToken = (4 * 2048 + 2 * 256 + 11008) * 2;
+// hidden, normalised x, rotated q, attention output (bf16 [2048] each) and
+// the SwiGLU output (bf16 [11008]); then the GEMMs' split-K scratch.  k and v
+// go straight into the caches.
+constexpr int64_t kPrefillBytesPerToken = (4 * 2048 + 11008) * 2;
 constexpr int64_t kPrefillFixedBytes = kGemmScratchFloats * 4;
 
 hipError_t model_prefill(const Model& m, uint8_t* ws, int64_t start, int64_t count, hipStream_t stream) {
@@ -467,9 +471,7 @@ hipError_t model_prefill(const Model& m, uint8_t* ws, int64_t start, int64_t cou
     uint16_t* hidden = reinterpret_cast<uint16_t*>(ws);
     uint16_t* xn = hidden + count * 2048;
     uint16_t* q = xn + count * 2048;
-    uint16_t* k = q + count * 2048;
-    uint16_t* v = k + count * 256;
-    uint16_t* attn = v + count * 256;
+    uint16_t* attn = q + count * 2048;
     uint16_t* mlp = attn + count * 2048;
     float* gemm_partials = reinterpret_cast<float*>(ws + count * kPrefillBytesPerToken);
     const float qk_scale_log2 = static_cast<float>(1.0 / std::sqrt(128.0)) * kLog2e;
@@ -510,30 +512,33 @@ hipError_t model_prefill(const Model& m, uint8_t* ws, int64_t start, int64_t cou
         }
         st = launch_prefill_norm(na, stream);
         if (st == hipSuccess) {
-            st = gemm(GemmEpi::kBias, xn, L[KUDACUDA_QWEN2_Q_PACKED], L[KUDACUDA_QWEN2_Q_ABSMAX], 0, 0,
-                      ptr<const uint16_t>(L[KUDACUDA_QWEN2_Q_BIAS]), q, 2048, 2048);
-        }
-        if (st == hipSuccess) {
-            st = gemm(GemmEpi::kBias, xn, L[KUDACUDA_QWEN2_K_PACKED], L[KUDACUDA_QWEN2_K_ABSMAX], 0, 0,
-                      ptr<const uint16_t>(L[KUDACUDA_QWEN2_K_BIAS]), k, 256, 2048);
-        }
-        if (st == hipSuccess) {
-            st = gemm(GemmEpi::kBias, xn, L[KUDACUDA_QWEN2_V_PACKED], L[KUDACUDA_QWEN2_V_ABSMAX], 0, 0,
-                      ptr<const uint16_t>(L[KUDACUDA_QWEN2_V_BIAS]), v, 256, 2048);
-        }
-        if (st == hipSuccess) {
-            PrefillRopeArgs ra;
-            ra.q = q;
-            ra.k = k;
-            ra.v = v;
-            ra.rope_cos = ptr<const float>(G[KUDACUDA_QWEN2_ROPE_COS]);
-            ra.rope_sin = ptr<const float>(G[KUDACUDA_QWEN2_ROPE_SIN]);
-            ra.kcache = ptr<uint16_t>(L[KUDACUDA_QWEN2_KEY_CACHE]);
-            ra.vcache = ptr<uint16_t>(L[KUDACUDA_QWEN2_VALUE_CACHE]);
-            ra.capacity = m.capacity;
-            ra.start = start;
-            ra.m = count;
-            st = launch_prefill_rope_cache(ra, stream);
+            // Q, K and V in one GEMM; its split reduce adds the biases, applies
+            // RoPE and writes k and v into the caches
+            Nf4GemmArgs a;
+            a.x = xn;
+            a.w[0] = ptr<const uint8_t>(L[KUDACUDA_QWEN2_Q_PACKED]);
+            a.w[1] = ptr<const uint8_t>(L[KUDACUDA_QWEN2_K_PACKED]);
+            a.w[2] = ptr<const uint8_t>(L[KUDACUDA_QWEN2_V_PACKED]);
+            a.absmax[0] = ptr<const float>(L[KUDACUDA_QWEN2_Q_ABSMAX]);
+            a.absmax[1] = ptr<const float>(L[KUDACUDA_QWEN2_K_ABSMAX]);
+            a.absmax[2] = ptr<const float>(L[KUDACUDA_QWEN2_V_ABSMAX]);
+            a.seg_bias[0] = ptr<const uint16_t>(L[KUDACUDA_QWEN2_Q_BIAS]);
+            a.seg_bias[1] = ptr<const uint16_t>(L[KUDACUDA_QWEN2_K_BIAS]);
+            a.seg_bias[2] = ptr<const uint16_t>(L[KUDACUDA_QWEN2_V_BIAS]);
+            a.out = q;
+            a.q_rows = 2048;
+            a.kv_rows = 256;
+            a.n = 2048 + 2 * 256;
+            a.k = 2048;
+            a.rope_cos = ptr<const float>(G[KUDACUDA_QWEN2_ROPE_COS]);
+            a.rope_sin = ptr<const float>(G[KUDACUDA_QWEN2_ROPE_SIN]);
+            a.kcache = ptr<uint16_t>(L[KUDACUDA_QWEN2_KEY_CACHE]);
+            a.vcache = ptr<uint16_t>(L[KUDACUDA_QWEN2_VALUE_CACHE]);
+            a.capacity = m.capacity;
+            a.start = start;
+            a.partials = gemm_partials;
+            a.partial_floats = kGemmScratchFloats;
+            st = gemm_chunks(GemmEpi::kQkvRope, a, count, stream);
         }
         if (st == hipSuccess) {
             PrefillAttnArgs aa;

@@ -200,7 +200,7 @@ def test_model_prefill_guards(torch_gpu, native, prefill_pair):
     lib = native.lib
     assert lib.kudacuda_qwen2_prefill_workspace_bytes(0) == 0
     # activations per token + the GEMMs' 16 MiB split-K scratch
-    assert lib.kudacuda_qwen2_prefill_workspace_bytes(3) == 3 * (4 * 2048 + 2 * 256 + 11008) * 2 + (16 << 20)
+    assert lib.kudacuda_qwen2_prefill_workspace_bytes(3) == 3 * (4 * 2048 + 11008) * 2 + (16 << 20)
     assert lib.kudacuda_qwen2_model_prefill(gpu.model, 0, 1 << 20, 0, 4, 0) == 1
     assert lib.kudacuda_qwen2_model_prefill(gpu.model, 1, 1 << 30, 60, 8, 0) == 1  # past kv_capacity 64
     assert b"kv_capacity" in lib.kudacuda_last_error(native.handle)

@@ -98,7 +98,7 @@ hipError_t launch_nf4_down11008(Act act, const Nf4DownArgs& args, hipStream_t st
 // x bf16 [m, k] row-major, weights in the bitsandbytes layout ([n, k/2] codes,
 // [n, k/64] fp32 absmax), fp32 accumulation.  m <= kGemmMaxTokens per launch,
 // n % 64 == 0, k % 128 == 0.
-enum class GemmEpi { kBias = 0, kResidual = 1, kSwiGlu = 2, kQkvRope = 3 };
+enum class GemmEpi { kBias = 0, kResidual = 1, kSwiGlu = 2, kQkvRope = 3, kResidualNorm = 4 };
 constexpr int kGemmMaxTokens = 64;
 // split-K scratch: fp32 partial tiles [weights][splits][m][n]
 constexpr int64_t kGemmScratchFloats = int64_t{4} << 20;
@@ -133,6 +133,12 @@ struct Nf4GemmArgs {
     uint16_t* vcache = nullptr;
     int64_t capacity = 0;
     int64_t start = 0;
+    // kResidualNorm (n = 2048, always split): out = bf16(residual +
+    // bf16(sum)) as kResidual, then, with norm_gamma, the row RMSNorm of the
+    // new out rows into norm_out (the prefill norm's arithmetic).
+    const uint16_t* norm_gamma = nullptr;
+    uint16_t* norm_out = nullptr;
+    float eps = 1e-6f;
 };
 hipError_t launch_nf4_gemm(GemmEpi epi, const Nf4GemmArgs& args, hipStream_t stream);
 

@@ -257,8 +257,8 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(Nf4GemmArgs a) {
         }
         return;
     }
-    if constexpr (EPI == GemmEpi::kQkvRope) {
-        return;  // always split: the epilogue is in qkv_rope_reduce_kernel
+    if constexpr (EPI == GemmEpi::kQkvRope || EPI == GemmEpi::kResidualNorm) {
+        return;  // always split: the epilogue is in the split reduce
     }
     floatx4 up[NT];
     if constexpr (kSw) {
@@ -437,6 +437,73 @@ __global__ __launch_bounds__(256) void qkv_rope_reduce_kernel(Nf4GemmArgs a, int
     *reinterpret_cast<uint32_t*>(dst + 64) = rh;
 }
 
+// kResidualNorm epilogue: one block per token row of 2048, thread t owns
+// columns 8t..8t+7.  Split partials summed in split order, the residual
+// epilogue bf16(res + bf16(sum)) written back to out, then (with norm_gamma)
+// the row's RMSNorm: fp32 sum of squares of the new bf16 row (8 fmaf per
+// thread, wave butterfly, the 4 wave sums (w0 + w1) + (w2 + w3)), the decode
+// kernels' inv_rms and bf16((h * inv) * gamma) into norm_out.
+__global__ __launch_bounds__(256) void residual_norm_reduce_kernel(Nf4GemmArgs a, int S) {
+    __shared__ float s_ss[4];
+    const int64_t m = blockIdx.x;
+    const int t = threadIdx.x;
+    const int64_t c = 8 * t;
+    const float* src = a.partials + m * a.n + c;
+    const int64_t plane = a.m * a.n;
+    float4 p0 = *reinterpret_cast<const float4*>(src);
+    float4 p1 = *reinterpret_cast<const float4*>(src + 4);
+    for (int s = 1; s < S; ++s) {
+        const float4 q0 = *reinterpret_cast<const float4*>(src + s * plane);
+        const float4 q1 = *reinterpret_cast<const float4*>(src + s * plane + 4);
+        p0.x = p0.x + q0.x;
+        p0.y = p0.y + q0.y;
+        p0.z = p0.z + q0.z;
+        p0.w = p0.w + q0.w;
+        p1.x = p1.x + q1.x;
+        p1.y = p1.y + q1.y;
+        p1.z = p1.z + q1.z;
+        p1.w = p1.w + q1.w;
+    }
+    const float v[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+    const uint4 rv = *reinterpret_cast<const uint4*>(a.residual + m * a.n + c);
+    float res[8];
+    unpack8<Bf16>(rv, res);
+    float h[8];
+    uint32_t packed[4];
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+        const uint16_t lo = Bf16::store(res[i] + Bf16::load(Bf16::store(v[i])));
+        const uint16_t hi = Bf16::store(res[i + 1] + Bf16::load(Bf16::store(v[i + 1])));
+        h[i] = Bf16::load(lo);
+        h[i + 1] = Bf16::load(hi);
+        packed[i / 2] = static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+    }
+    *reinterpret_cast<uint4*>(a.out + m * a.n + c) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    if (a.norm_gamma == nullptr) {
+        return;
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        ss = fmaf(h[i], h[i], ss);
+    }
+    ss = wave_sum(ss);
+    if ((t & 63) == 0) {
+        s_ss[t >> 6] = ss;
+    }
+    __syncthreads();
+    const float r = inv_rms((s_ss[0] + s_ss[1]) + (s_ss[2] + s_ss[3]), 2048.0f, a.eps);
+    float g[8];
+    unpack8<Bf16>(*reinterpret_cast<const uint4*>(a.norm_gamma + c), g);
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+        const uint32_t lo = Bf16::store((h[i] * r) * g[i]);
+        const uint32_t hi = Bf16::store((h[i + 1] * r) * g[i + 1]);
+        packed[i / 2] = lo | (hi << 16);
+    }
+    *reinterpret_cast<uint4*>(a.norm_out + m * a.n + c) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+}
+
 template <GemmEpi EPI>
 hipError_t launch_gemm_epi(const Nf4GemmArgs& a, hipStream_t stream) {
     constexpr int NF = EPI == GemmEpi::kSwiGlu ? 2 : 1;
@@ -452,7 +519,7 @@ hipError_t launch_gemm_epi(const Nf4GemmArgs& a, hipStream_t stream) {
         while (S > 1 && NF * S * a.m * a.n > a.partial_floats) {
             --S;
         }
-        if (EPI == GemmEpi::kQkvRope && S < 2) {
+        if ((EPI == GemmEpi::kQkvRope || EPI == GemmEpi::kResidualNorm) && S < 2) {
             S = 2;
         }
         if (S > 1) {
@@ -484,6 +551,9 @@ hipError_t launch_gemm_epi(const Nf4GemmArgs& a, hipStream_t stream) {
     if constexpr (EPI == GemmEpi::kQkvRope) {
         hipLaunchKernelGGL(qkv_rope_reduce_kernel, dim3(static_cast<unsigned>((quads + 255) / 256)), dim3(256), 0,
                            stream, a, static_cast<int>(S));
+    } else if constexpr (EPI == GemmEpi::kResidualNorm) {
+        hipLaunchKernelGGL(residual_norm_reduce_kernel, dim3(static_cast<unsigned>(a.m)), dim3(256), 0, stream, a,
+                           static_cast<int>(S));
     } else {
         hipLaunchKernelGGL(gemm_reduce_kernel<EPI>, dim3(static_cast<unsigned>((quads + 255) / 256)), dim3(256), 0,
                            stream, a, static_cast<int>(S));
@@ -497,7 +567,12 @@ hipError_t launch_nf4_gemm(GemmEpi epi, const Nf4GemmArgs& a, hipStream_t stream
     if (a.m < 1 || a.m > kGemmMaxTokens || a.n < kRowsPerBlock || a.n % kRowsPerBlock != 0 || a.k < kWindow ||
         a.k % kWindow != 0 || a.x == nullptr || a.w[0] == nullptr || a.absmax[0] == nullptr || a.out == nullptr ||
         (epi == GemmEpi::kSwiGlu && (a.w[1] == nullptr || a.absmax[1] == nullptr)) ||
-        (epi == GemmEpi::kResidual && a.residual == nullptr)) {
+        ((epi == GemmEpi::kResidual || epi == GemmEpi::kResidualNorm) && a.residual == nullptr)) {
+        return hipErrorInvalidValue;
+    }
+    if (epi == GemmEpi::kResidualNorm &&
+        (a.partials == nullptr || a.n != 2048 || 2 * a.m * a.n > a.partial_floats ||
+         (a.norm_gamma != nullptr && a.norm_out == nullptr))) {
         return hipErrorInvalidValue;
     }
     if (epi == GemmEpi::kQkvRope &&
@@ -517,6 +592,8 @@ hipError_t launch_nf4_gemm(GemmEpi epi, const Nf4GemmArgs& a, hipStream_t stream
             return launch_gemm_epi<GemmEpi::kSwiGlu>(a, stream);
         case GemmEpi::kQkvRope:
             return launch_gemm_epi<GemmEpi::kQkvRope>(a, stream);
+        case GemmEpi::kResidualNorm:
+            return launch_gemm_epi<GemmEpi::kResidualNorm>(a, stream);
     }
     return hipErrorInvalidValue;
 }

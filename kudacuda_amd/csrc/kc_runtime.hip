@@ -440,6 +440,7 @@ hipError_t gemm_chunks(GemmEpi epi, Nf4GemmArgs a, int64_t tokens, hipStream_t s
     const uint16_t* x = a.x;
     const uint16_t* res = a.residual;
     uint16_t* out = a.out;
+    uint16_t* norm_out = a.norm_out;
     const int64_t start = a.start;
     const int64_t out_stride = epi == GemmEpi::kQkvRope ? a.q_rows : a.n;
     for (int64_t m0 = 0; m0 < tokens; m0 += kGemmMaxTokens) {
@@ -447,6 +448,7 @@ hipError_t gemm_chunks(GemmEpi epi, Nf4GemmArgs a, int64_t tokens, hipStream_t s
         a.x = x + m0 * a.k;
         a.residual = res != nullptr ? res + m0 * a.n : nullptr;
         a.out = out + m0 * out_stride;
+        a.norm_out = norm_out != nullptr ? norm_out + m0 * a.n : nullptr;
         a.start = start + m0;
         const hipError_t status = launch_nf4_gemm(epi, a, stream);
         if (status != hipSuccess) {
@@ -476,41 +478,45 @@ hipError_t model_prefill(const Model& m, uint8_t* ws, int64_t start, int64_t cou
     float* gemm_partials = reinterpret_cast<float*>(ws + count * kPrefillBytesPerToken);
     const float qk_scale_log2 = static_cast<float>(1.0 / std::sqrt(128.0)) * kLog2e;
     hipError_t st = hipSuccess;
+    // kResidualNorm: out += the product (residual stream in place), then the
+    // row RMSNorm with `gamma` (null: none) into xn for the next GEMM
     auto gemm = [&](GemmEpi epi, const uint16_t* x, uint64_t w0, uint64_t a0, uint64_t w1, uint64_t a1,
-                    const uint16_t* bias, uint16_t* out, int64_t n, int64_t kdim) {
+                    uint16_t* out, int64_t n, int64_t kdim, const uint16_t* gamma) {
         Nf4GemmArgs a;
         a.x = x;
         a.w[0] = ptr<const uint8_t>(w0);
         a.absmax[0] = ptr<const float>(a0);
         a.w[1] = ptr<const uint8_t>(w1);
         a.absmax[1] = ptr<const float>(a1);
-        a.bias = bias;
-        a.residual = epi == GemmEpi::kResidual ? out : nullptr;
+        a.residual = epi == GemmEpi::kResidualNorm ? out : nullptr;
         a.out = out;
         a.n = n;
         a.k = kdim;
         a.partials = gemm_partials;
         a.partial_floats = kGemmScratchFloats;
+        a.norm_gamma = gamma;
+        a.norm_out = gamma != nullptr ? xn : nullptr;
+        a.eps = m.eps;
         return gemm_chunks(epi, a, count, stream);
     };
     for (int64_t layer = 0; layer < m.num_layers && st == hipSuccess; ++layer) {
         const auto& L = m.layers[static_cast<size_t>(layer)];
-        PrefillNormArgs na;
-        na.gamma = ptr<const uint16_t>(L[KUDACUDA_QWEN2_INPUT_NORM]);
-        na.eps = m.eps;
-        na.out = xn;
-        na.m = count;
         if (layer == 0) {
+            // embedding rows -> hidden, input norm -> xn (later layers get xn
+            // from the previous layer's down-projection reduce)
+            PrefillNormArgs na;
+            na.gamma = ptr<const uint16_t>(L[KUDACUDA_QWEN2_INPUT_NORM]);
+            na.eps = m.eps;
+            na.out = xn;
+            na.m = count;
             na.embed = ptr<const uint16_t>(G[KUDACUDA_QWEN2_EMBED]);
             na.tokens = ptr<const int32_t>(G[KUDACUDA_QWEN2_TOKENS]);
             na.control = ptr<const int32_t>(G[KUDACUDA_QWEN2_CONTROL]);
             na.vocab = m.vocab;
             na.start = start;
             na.hidden_out = hidden;
-        } else {
-            na.x = hidden;
+            st = launch_prefill_norm(na, stream);
         }
-        st = launch_prefill_norm(na, stream);
         if (st == hipSuccess) {
             // Q, K and V in one GEMM; its split reduce adds the biases, applies
             // RoPE and writes k and v into the caches
@@ -553,25 +559,19 @@ hipError_t model_prefill(const Model& m, uint8_t* ws, int64_t start, int64_t cou
             st = launch_prefill_attention(aa, stream);
         }
         if (st == hipSuccess) {
-            st = gemm(GemmEpi::kResidual, attn, L[KUDACUDA_QWEN2_O_PACKED], L[KUDACUDA_QWEN2_O_ABSMAX], 0, 0,
-                      nullptr, hidden, 2048, 2048);
-        }
-        if (st == hipSuccess) {
-            PrefillNormArgs pa;
-            pa.x = hidden;
-            pa.gamma = ptr<const uint16_t>(L[KUDACUDA_QWEN2_POST_NORM]);
-            pa.eps = m.eps;
-            pa.out = xn;
-            pa.m = count;
-            st = launch_prefill_norm(pa, stream);
+            st = gemm(GemmEpi::kResidualNorm, attn, L[KUDACUDA_QWEN2_O_PACKED], L[KUDACUDA_QWEN2_O_ABSMAX], 0, 0,
+                      hidden, 2048, 2048, ptr<const uint16_t>(L[KUDACUDA_QWEN2_POST_NORM]));
         }
         if (st == hipSuccess) {
             st = gemm(GemmEpi::kSwiGlu, xn, L[KUDACUDA_QWEN2_GATE_PACKED], L[KUDACUDA_QWEN2_GATE_ABSMAX],
-                      L[KUDACUDA_QWEN2_UP_PACKED], L[KUDACUDA_QWEN2_UP_ABSMAX], nullptr, mlp, 11008, 2048);
+                      L[KUDACUDA_QWEN2_UP_PACKED], L[KUDACUDA_QWEN2_UP_ABSMAX], mlp, 11008, 2048, nullptr);
         }
         if (st == hipSuccess) {
-            st = gemm(GemmEpi::kResidual, mlp, L[KUDACUDA_QWEN2_DOWN_PACKED], L[KUDACUDA_QWEN2_DOWN_ABSMAX], 0, 0,
-                      nullptr, hidden, 2048, 11008);
+            const bool last = layer + 1 == m.num_layers;
+            const uint16_t* next_norm =
+                last ? nullptr : ptr<const uint16_t>(m.layers[static_cast<size_t>(layer + 1)][KUDACUDA_QWEN2_INPUT_NORM]);
+            st = gemm(GemmEpi::kResidualNorm, mlp, L[KUDACUDA_QWEN2_DOWN_PACKED], L[KUDACUDA_QWEN2_DOWN_ABSMAX], 0, 0,
+                      hidden, 2048, 11008, next_norm);
         }
     }
     if (st != hipSuccess) {

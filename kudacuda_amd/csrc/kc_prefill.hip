@@ -314,6 +314,37 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(Nf4GemmArgs a) {
     }
 }
 
+// Sum of the S split partials of V consecutive floats at `src` (splits
+// `plane` floats apart) in split order.  The loads of up to 8 splits are
+// issued together (split index clamped; the clamped repeats are not added),
+// so S splits cost ceil((S - 1) / 8) memory round trips instead of S - 1.
+template <int V>
+__device__ __forceinline__ void split_sum(const float* src, int64_t plane, int S, float* out) {
+    typedef float vec __attribute__((ext_vector_type(V)));
+    vec acc = *reinterpret_cast<const vec*>(src);
+    for (int s0 = 1; s0 < S; s0 += 8) {
+        vec p[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int s = s0 + j < S ? s0 + j : S - 1;
+            p[j] = *reinterpret_cast<const vec*>(src + s * plane);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (s0 + j < S) {
+#pragma unroll
+                for (int i = 0; i < V; ++i) {
+                    acc[i] = acc[i] + p[j][i];
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        out[i] = acc[i];
+    }
+}
+
 // One thread per 4 consecutive outputs of one token: the split partials are
 // summed in split order (fp32), then the GEMM's epilogue.
 template <GemmEpi EPI>
@@ -330,18 +361,7 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(Nf4GemmArgs a, int S) 
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
         const float* src = a.partials + (static_cast<int64_t>(f) * S * a.m + m) * a.n + nb;
-        float4 acc = *reinterpret_cast<const float4*>(src);
-        for (int s = 1; s < S; ++s) {
-            const float4 p = *reinterpret_cast<const float4*>(src + static_cast<int64_t>(s) * a.m * a.n);
-            acc.x = acc.x + p.x;
-            acc.y = acc.y + p.y;
-            acc.z = acc.z + p.z;
-            acc.w = acc.w + p.w;
-        }
-        v[f][0] = acc.x;
-        v[f][1] = acc.y;
-        v[f][2] = acc.z;
-        v[f][3] = acc.w;
+        split_sum<4>(src, a.m * a.n, S, v[f]);
     }
     uint16_t h[4];
 #pragma unroll
@@ -382,17 +402,10 @@ __global__ __launch_bounds__(256) void qkv_rope_reduce_kernel(Nf4GemmArgs a, int
     const int64_t plane = a.m * a.n;
     if (u >= q_units + k_units) {
         const int64_t c = a.q_rows + a.kv_rows + 4 * (u - q_units - k_units);  // v column
-        float4 acc = *reinterpret_cast<const float4*>(src + c);
-        for (int s = 1; s < S; ++s) {
-            const float4 p = *reinterpret_cast<const float4*>(src + s * plane + c);
-            acc.x = acc.x + p.x;
-            acc.y = acc.y + p.y;
-            acc.z = acc.z + p.z;
-            acc.w = acc.w + p.w;
-        }
+        float vs[4];
+        split_sum<4>(src + c, plane, S, vs);
         const int64_t cv = c - a.q_rows - a.kv_rows;
         const uint16_t* b = a.seg_bias[2];
-        const float vs[4] = {acc.x, acc.y, acc.z, acc.w};
         uint16_t h[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -408,16 +421,11 @@ __global__ __launch_bounds__(256) void qkv_rope_reduce_kernel(Nf4GemmArgs a, int
     const int64_t head = uu / 32;
     const int d = static_cast<int>(uu % 32) * 2;
     const int64_t c0 = (is_q ? 0 : a.q_rows) + head * 128 + d;  // partial column of (d, d + 1)
-    float2 lo = *reinterpret_cast<const float2*>(src + c0);
-    float2 hi = *reinterpret_cast<const float2*>(src + c0 + 64);
-    for (int s = 1; s < S; ++s) {
-        const float2 pl = *reinterpret_cast<const float2*>(src + s * plane + c0);
-        const float2 ph = *reinterpret_cast<const float2*>(src + s * plane + c0 + 64);
-        lo.x = lo.x + pl.x;
-        lo.y = lo.y + pl.y;
-        hi.x = hi.x + ph.x;
-        hi.y = hi.y + ph.y;
-    }
+    float lov[2], hiv[2];
+    split_sum<2>(src + c0, plane, S, lov);
+    split_sum<2>(src + c0 + 64, plane, S, hiv);
+    const float2 lo = make_float2(lov[0], lov[1]);
+    const float2 hi = make_float2(hiv[0], hiv[1]);
     const uint16_t* b = is_q ? a.seg_bias[0] : a.seg_bias[1];
     const int64_t cb0 = head * 128 + d;  // column within the segment
     const float l0 = Bf16::load(Bf16::store(b != nullptr ? lo.x + Bf16::load(b[cb0]) : lo.x));
@@ -450,21 +458,8 @@ __global__ __launch_bounds__(256) void residual_norm_reduce_kernel(Nf4GemmArgs a
     const int64_t c = 8 * t;
     const float* src = a.partials + m * a.n + c;
     const int64_t plane = a.m * a.n;
-    float4 p0 = *reinterpret_cast<const float4*>(src);
-    float4 p1 = *reinterpret_cast<const float4*>(src + 4);
-    for (int s = 1; s < S; ++s) {
-        const float4 q0 = *reinterpret_cast<const float4*>(src + s * plane);
-        const float4 q1 = *reinterpret_cast<const float4*>(src + s * plane + 4);
-        p0.x = p0.x + q0.x;
-        p0.y = p0.y + q0.y;
-        p0.z = p0.z + q0.z;
-        p0.w = p0.w + q0.w;
-        p1.x = p1.x + q1.x;
-        p1.y = p1.y + q1.y;
-        p1.z = p1.z + q1.z;
-        p1.w = p1.w + q1.w;
-    }
-    const float v[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+    float v[8];
+    split_sum<8>(src, plane, S, v);
     const uint4 rv = *reinterpret_cast<const uint4*>(a.residual + m * a.n + c);
     float res[8];
     unpack8<Bf16>(rv, res);

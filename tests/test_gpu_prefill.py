@@ -166,6 +166,45 @@ def test_model_prefill_matches_the_host_restatement(torch_gpu, prefill_pair):
         assert tokens[PROMPT_LEN] == ref["token"]
 
 
+LONG_KW = dict(num_layers=2, vocab=4096, kv_capacity=128, token_capacity=128)
+LONG_PROMPT = 100  # two 64-token GEMM chunks (the second one ragged), causal rounds of 32 past 64
+
+
+def test_model_prefill_of_a_multi_chunk_prompt(torch_gpu, native):
+    """A prompt longer than one GEMM launch: the second chunk's rows (and its
+    RoPE positions 64..99) and attention over 100 cached rows."""
+
+    from kudacuda_amd import synthetic
+    from kudacuda_amd.qwen2_decoder import Qwen2Nf4Decoder
+    from tests._host_model import HostModel
+    from tests._prefill_ref import prefill_reference
+
+    gpu = Qwen2Nf4Decoder.synthetic(native, torch_gpu, seed=SEED + 7, **LONG_KW)
+    try:
+        cpu = HostModel(SEED + 7, **LONG_KW)
+        prompt = synthetic.prompt_ids(SEED + 7, LONG_PROMPT, LONG_KW["vocab"])
+        print(f"model prefill of {LONG_PROMPT} tokens, 2 layers", flush=True)
+        gpu.prefill(prompt)
+        gpu.stream.synchronize()
+        ref = prefill_reference(cpu, prompt)
+        for li in range(LONG_KW["num_layers"]):
+            for name in ("key_cache", "value_cache"):
+                got = O.bf16_to_f32(host(gpu.layers[li][name]).reshape(2, -1, 128)[:, :LONG_PROMPT])
+                want = (ref["kcache"] if name == "key_cache" else ref["vcache"])[li]
+                _rel_close(got, want, f"layer {li} {name}")
+        got_logits = O.bf16_to_f32(host(gpu.logits))
+        want_logits = O.bf16_to_f32(ref["logits"])
+        err = float(np.abs(got_logits - want_logits).max())
+        print(f"last-row logits: max |diff| {err:.4g}", flush=True)
+        assert err <= 0.05
+        assert host(gpu.control)[0] == LONG_PROMPT
+        top2 = np.sort(want_logits)[-2:]
+        if top2[1] - top2[0] > 2 * err:
+            assert host(gpu.tokens)[LONG_PROMPT] == ref["token"]
+    finally:
+        gpu.close()
+
+
 def test_decode_continues_bit_exactly_from_the_prefilled_state(torch_gpu, prefill_pair):
     """After a GPU prefill, decode steps on the GPU and oracle decode steps on
     the CPU started from the same state (the prefilled KV rows and token)

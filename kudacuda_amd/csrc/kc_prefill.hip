@@ -570,6 +570,10 @@ hipError_t launch_nf4_gemm(GemmEpi epi, const Nf4GemmArgs& a, hipStream_t stream
          (a.norm_gamma != nullptr && a.norm_out == nullptr))) {
         return hipErrorInvalidValue;
     }
+    // the split-only epilogues need two windows at least (two splits)
+    if ((epi == GemmEpi::kQkvRope || epi == GemmEpi::kResidualNorm) && a.k < 2 * kWindow) {
+        return hipErrorInvalidValue;
+    }
     if (epi == GemmEpi::kQkvRope &&
         (a.partials == nullptr || a.q_rows < 128 || a.q_rows % 128 != 0 || a.kv_rows < 128 || a.kv_rows % 128 != 0 ||
          a.n != a.q_rows + 2 * a.kv_rows || a.w[1] == nullptr || a.w[2] == nullptr || a.absmax[1] == nullptr ||

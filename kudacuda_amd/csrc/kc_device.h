@@ -168,36 +168,47 @@ __device__ __forceinline__ float load_agent(const float* p) {
 __device__ __forceinline__ void wait_own_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // ------------------------------------------------------------------ NF4 dots
-// v_bfe_u32 with a constant field: written as asm because the compiler
-// otherwise rewrites a chain of byte extracts of a pre-masked word back into a
-// shift and a mask per byte.
-template <int OFF>
-__device__ __forceinline__ uint32_t bfe8(uint32_t v) {
+// (byte B of x) & 0x3c in one instruction (a byte-select AND), written as asm:
+// the compiler folds a byte-select AND back into a shift and an AND.
+template <int B>
+__device__ __forceinline__ uint32_t byte_and_3c(uint32_t x) {
     uint32_t r;
-    asm("v_bfe_u32 %0, %1, %2, 8" : "=v"(r) : "v"(v), "i"(OFF));
+    if constexpr (B == 0) {
+        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
+            : "=v"(r) : "v"(0x3cu), "v"(x));
+    } else if constexpr (B == 1) {
+        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1"
+            : "=v"(r) : "v"(0x3cu), "v"(x));
+    } else if constexpr (B == 2) {
+        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2"
+            : "=v"(r) : "v"(0x3cu), "v"(x));
+    } else {
+        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3"
+            : "=v"(r) : "v"(0x3cu), "v"(x));
+    }
     return r;
 }
 
 // Codebook values of the 32 codes of one chunk, gathered from the LDS table
-// before any arithmetic so the lookups overlap.  For each 32-bit word the
-// byte offsets code*4 of the high and low nibbles come from one shift and one
-// mask each ((w >> 2) & 0x3c..., (w << 2) & 0x3c...).
+// before any arithmetic so the lookups overlap.  The byte offsets code*4 come
+// from two shifted copies of each 32-bit word: byte b of (w >> 2) holds the
+// high nibble of byte b at bits 2..5, byte b of (w << 2) the low nibble, so
+// each offset is one byte-select AND.
 __device__ __forceinline__ void nf4_gather32(const uint4 pk, const float* cb, float* cw) {
     const uint32_t w[4] = {pk.x, pk.y, pk.z, pk.w};
     const char* base = reinterpret_cast<const char*>(cb);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t hi4 = (w[i] >> 2) & 0x3c3c3c3cu;
-        const uint32_t lo4 = (w[i] << 2) & 0x3c3c3c3cu;
-        // one bitfield extract per code, offsets already scaled by 4
-        cw[8 * i + 0] = *reinterpret_cast<const float*>(base + bfe8<0>(hi4));
-        cw[8 * i + 1] = *reinterpret_cast<const float*>(base + bfe8<0>(lo4));
-        cw[8 * i + 2] = *reinterpret_cast<const float*>(base + bfe8<8>(hi4));
-        cw[8 * i + 3] = *reinterpret_cast<const float*>(base + bfe8<8>(lo4));
-        cw[8 * i + 4] = *reinterpret_cast<const float*>(base + bfe8<16>(hi4));
-        cw[8 * i + 5] = *reinterpret_cast<const float*>(base + bfe8<16>(lo4));
-        cw[8 * i + 6] = *reinterpret_cast<const float*>(base + bfe8<24>(hi4));
-        cw[8 * i + 7] = *reinterpret_cast<const float*>(base + bfe8<24>(lo4));
+        const uint32_t hi4 = w[i] >> 2;
+        const uint32_t lo4 = w[i] << 2;
+        cw[8 * i + 0] = *reinterpret_cast<const float*>(base + byte_and_3c<0>(hi4));
+        cw[8 * i + 1] = *reinterpret_cast<const float*>(base + byte_and_3c<0>(lo4));
+        cw[8 * i + 2] = *reinterpret_cast<const float*>(base + byte_and_3c<1>(hi4));
+        cw[8 * i + 3] = *reinterpret_cast<const float*>(base + byte_and_3c<1>(lo4));
+        cw[8 * i + 4] = *reinterpret_cast<const float*>(base + byte_and_3c<2>(hi4));
+        cw[8 * i + 5] = *reinterpret_cast<const float*>(base + byte_and_3c<2>(lo4));
+        cw[8 * i + 6] = *reinterpret_cast<const float*>(base + byte_and_3c<3>(hi4));
+        cw[8 * i + 7] = *reinterpret_cast<const float*>(base + byte_and_3c<3>(lo4));
     }
 }
 

@@ -58,28 +58,8 @@ __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast
 // v_cvt_pk_bf16_f32; the products are finite); element j lands in slot j.
 // The codebook byte offsets (4 * code) come from two shifted copies of the
 // word: byte b of (word >> 2) holds the high nibble of byte b at bits 2..5,
-// byte b of (word << 2) the low nibble, so each offset is one byte-select AND.
-// (written as asm: the compiler folds a byte-select AND back into a shift and
-// an AND).
-template <int B>
-__device__ __forceinline__ uint32_t byte_and_3c(uint32_t x) {
-    uint32_t r;
-    if constexpr (B == 0) {
-        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
-            : "=v"(r) : "v"(0x3cu), "v"(x));
-    } else if constexpr (B == 1) {
-        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1"
-            : "=v"(r) : "v"(0x3cu), "v"(x));
-    } else if constexpr (B == 2) {
-        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2"
-            : "=v"(r) : "v"(0x3cu), "v"(x));
-    } else {
-        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3"
-            : "=v"(r) : "v"(0x3cu), "v"(x));
-    }
-    return r;
-}
-
+// byte b of (word << 2) the low nibble, so each offset is one byte-select AND
+// (byte_and_3c).
 template <int B>
 __device__ __forceinline__ void dequant_byte(bf16x8& v, uint32_t hi4, uint32_t lo4, float am, const char* base) {
     const uint32_t oh = byte_and_3c<B>(hi4);

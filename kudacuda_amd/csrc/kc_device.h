@@ -53,7 +53,12 @@ __device__ __forceinline__ float f16_to_f32(uint16_t v) {
     return static_cast<float>(__builtin_bit_cast(_Float16, v));
 }
 
+// fp32 -> fp16, round to nearest even.  The value passes through an empty asm
+// first: otherwise the compiler folds a preceding fp32 multiply into a
+// mixed-precision FMA that rounds the exact product to fp16 once, which
+// differs from rounding the fp32 product when that product is an fp16 tie.
 __device__ __forceinline__ uint16_t f32_to_f16(float f) {
+    asm volatile("" : "+v"(f));
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 }
 

@@ -24,6 +24,7 @@ namespace kc {
 namespace {
 
 constexpr int kRowsThreads = 256;
+constexpr int kNormPitch = 36;  // floats per lane row of the shared norm (32 + 4: conflict-free)
 // Row-kernel launch cap: up to 6144 waves (24 per CU on 256 CUs), so a
 // wave owns at most 2 tasks of the 11008-task gate/up and the rest own 1;
 // measured faster than fewer waves with more tasks each (the dequant is
@@ -183,8 +184,14 @@ template <typename T, RowMode MODE, int TPW, bool ATTN = false>
 __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs a, int64_t ntasks) {
     static_assert(!ATTN || MODE == RowMode::kGemv, "attention merge feeds the GEMV only");
     static_assert(!ATTN || kRowsThreads * 8 == 2048, "one thread per 8 merged outputs");
+    // kQkv / kQkvRope / kSwiGlu: the block's 4 waves share the RMSNorm (each
+    // normalises a quarter of the vector, through LDS)
+    constexpr bool kCoop = MODE != RowMode::kGemv;
+    static_assert(!kCoop || kRowsThreads == 256, "four waves share the norm");
     __shared__ float cb[16];
     __shared__ __attribute__((aligned(16))) uint16_t s_xa[ATTN ? 2048 : 8];
+    __shared__ float s_ss[4];
+    __shared__ __attribute__((aligned(16))) float s_xn[kCoop ? 64 * kNormPitch : 4];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t waves_per_block = kRowsThreads / 64;
@@ -225,17 +232,24 @@ __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs 
             }
         }
     }
-    const uint4* xv = reinterpret_cast<const uint4*>(x) + lane * 4;
-    const uint4* gv = reinterpret_cast<const uint4*>(has_gamma ? a.gamma : x) + lane * 4;
-    uint4 xr[4], gr[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        xr[i] = xv[i];
-    }
-    if constexpr (!ATTN) {
+    // kCoop: lane l of wave w holds elements 512w + 8l .. +7 (xq, gq);
+    // otherwise the lane's own 32 elements [32l, 32l + 32) (xr, gr)
+    uint4 xr[4], gr[4], xq, gq;
+    if constexpr (kCoop) {
+        xq = reinterpret_cast<const uint4*>(x)[64 * wave + lane];
+        gq = reinterpret_cast<const uint4*>(has_gamma ? a.gamma : x)[64 * wave + lane];
+    } else {
+        const uint4* xv = reinterpret_cast<const uint4*>(x) + lane * 4;
+        const uint4* gv = reinterpret_cast<const uint4*>(has_gamma ? a.gamma : x) + lane * 4;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            gr[i] = gv[i];
+            xr[i] = xv[i];
+        }
+        if constexpr (!ATTN) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                gr[i] = gv[i];
+            }
         }
     }
 
@@ -314,6 +328,21 @@ __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs 
             }
         }
     }
+    float xq8[8];
+    if constexpr (kCoop) {
+        // this wave's quarter of the sum of squares (8 fmaf per lane, wave
+        // butterfly); the four quarters meet in LDS behind the codebook barrier
+        unpack8<T>(xq, xq8);
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            acc = fmaf(xq8[j], xq8[j], acc);
+        }
+        acc = wave_sum(acc);
+        if (lane == 0) {
+            s_ss[wave] = acc;
+        }
+    }
     block_codebook_lds(cb);
     __syncthreads();
     if constexpr (ATTN) {
@@ -327,19 +356,47 @@ __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs 
 
     // RMSNorm of the lane's 32 elements against the whole vector
     float xn[32];
+    if constexpr (kCoop) {
+        // r from the four quarter sums ((w0 + w1) + (w2 + w3)); this lane
+        // normalises its 8 elements into the padded LDS row of their owner
+        // lane (elements [32L, 32L + 32) at s_xn[L * kNormPitch]), then every
+        // lane reads its own 32
+        const float r = inv_rms((s_ss[0] + s_ss[1]) + (s_ss[2] + s_ss[3]), 2048.0f, a.eps);
+        float g8[8];
+        unpack8<T>(gq, g8);
+        float y[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        unpack8<T>(xr[i], xn + 8 * i);
-    }
-    if (has_gamma) {
-        const float r = inv_rms(wave_sum(sumsq32(xn)), 2048.0f, a.eps);
+        for (int j = 0; j < 8; ++j) {
+            y[j] = has_gamma ? (xq8[j] * r) * g8[j] : xq8[j];
+        }
+        float* dst = s_xn + (16 * wave + (lane >> 2)) * kNormPitch + 8 * (lane & 3);
+        reinterpret_cast<float4*>(dst)[0] = make_float4(y[0], y[1], y[2], y[3]);
+        reinterpret_cast<float4*>(dst)[1] = make_float4(y[4], y[5], y[6], y[7]);
+        __syncthreads();
+        const float4* src = reinterpret_cast<const float4*>(s_xn + lane * kNormPitch);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float4 v = src[i];
+            xn[4 * i] = v.x;
+            xn[4 * i + 1] = v.y;
+            xn[4 * i + 2] = v.z;
+            xn[4 * i + 3] = v.w;
+        }
+    } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            float g[8];
-            unpack8<T>(gr[i], g);
+            unpack8<T>(xr[i], xn + 8 * i);
+        }
+        if (has_gamma) {
+            const float r = inv_rms(wave_sum(sumsq32(xn)), 2048.0f, a.eps);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                xn[8 * i + j] = (xn[8 * i + j] * r) * g[j];
+            for (int i = 0; i < 4; ++i) {
+                float g[8];
+                unpack8<T>(gr[i], g);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    xn[8 * i + j] = (xn[8 * i + j] * r) * g[j];
+                }
             }
         }
     }
@@ -356,14 +413,18 @@ __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs 
         }
     }
 
-    if (blockIdx.x == 0 && wave == 0) {
-        if (a.hidden_out != nullptr) {
+    if (blockIdx.x == 0 && a.hidden_out != nullptr) {
+        if constexpr (kCoop) {
+            reinterpret_cast<uint4*>(a.hidden_out)[64 * wave + lane] = xq;
+        } else if (wave == 0) {
             uint4* dst = reinterpret_cast<uint4*>(a.hidden_out) + lane * 4;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 dst[i] = xr[i];
             }
         }
+    }
+    if (blockIdx.x == 0 && wave == 0) {
         if (a.norm_out != nullptr) {
             float4* dst = reinterpret_cast<float4*>(a.norm_out) + lane * 8;
 #pragma unroll

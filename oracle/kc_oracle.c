@@ -166,13 +166,25 @@ static inline float sumsq32(const float* x) {
 
 static inline float inv_rms(float ss, float n, float eps) { return 1.0f / sqrtf(ss / n + eps); }
 
-/* x (2048, 16-bit) -> xn fp32 laid out lane-major (lane l owns [32l, 32l+32)). */
+/* x (2048, 16-bit) -> xn fp32 laid out lane-major (lane l owns [32l, 32l+32)).
+ * Sum of squares in the block-shared order of the GEMV/QKV/SwiGLU kernels:
+ * wave w (0..3) covers [512w, 512w + 512), its lane l the 8 elements
+ * 512w + 8l .. +7 (one fmaf chain), a 64-lane butterfly per wave, then
+ * (w0 + w1) + (w2 + w3). */
 static void norm_x2048(int act, const uint16_t* x, const uint16_t* gamma, float eps, float* xn) {
     for (int i = 0; i < 2048; ++i) xn[i] = act_load(act, x[i]);
     if (gamma == NULL) return;
-    float part[64];
-    for (int l = 0; l < 64; ++l) part[l] = sumsq32(xn + 32 * l);
-    const float r = inv_rms(butterfly(part, 64), 2048.0f, eps);
+    float ws[4];
+    for (int w = 0; w < 4; ++w) {
+        float part[64];
+        for (int l = 0; l < 64; ++l) {
+            float acc = 0.0f;
+            for (int j = 0; j < 8; ++j) acc = fmaf(xn[512 * w + 8 * l + j], xn[512 * w + 8 * l + j], acc);
+            part[l] = acc;
+        }
+        ws[w] = butterfly(part, 64);
+    }
+    const float r = inv_rms((ws[0] + ws[1]) + (ws[2] + ws[3]), 2048.0f, eps);
     for (int i = 0; i < 2048; ++i) xn[i] = (xn[i] * r) * act_load(act, gamma[i]);
 }
 

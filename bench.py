@@ -82,6 +82,17 @@ def step_bytes(cfg, vocab: int, kv_len: int) -> int:
     return cfg.layers * per_layer + b["lm_head"]
 
 
+def _cpu_model() -> str:
+    """Host CPU model name and logical CPU count (from /proc/cpuinfo)."""
+
+    try:
+        names = [line.split(":", 1)[1].strip() for line in open("/proc/cpuinfo", encoding="utf-8")
+                 if line.startswith("model name")]
+    except OSError:
+        return "unknown"
+    return f"{names[0]} ({len(names)} logical CPUs visible)" if names else "unknown"
+
+
 def cpu_baseline(seconds: float, threads: int) -> dict:
     """Time the oracle's decode step (same model, same math) on host cores."""
 
@@ -107,6 +118,7 @@ def cpu_baseline(seconds: float, threads: int) -> dict:
         "value": steps / elapsed,
         "unit": "tok/s",
         "cores": threads,
+        "cpu": _cpu_model(),
         "kind": "port",
         "sample": f"{steps} full decode steps (36 layers + lm_head/argmax, positions 0..{steps - 1}) of the same "
                   f"seeded model by oracle/kc_oracle.c with OpenMP, {elapsed:.1f}s timed, model build {build_s:.0f}s "

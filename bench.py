@@ -115,7 +115,7 @@ def cpu_baseline(seconds: float, threads: int) -> dict:
         if steps >= 2 and elapsed >= seconds:
             break
     return {
-        "value": steps / elapsed,
+        "value": round(steps / elapsed, 3),
         "unit": "tok/s",
         "cores": threads,
         "cpu": _cpu_model(),

@@ -194,34 +194,57 @@ __device__ __forceinline__ uint32_t byte_and_3c(uint32_t x) {
     return r;
 }
 
-// Codebook values of the 32 codes of one chunk, gathered from the LDS table
-// before any arithmetic so the lookups overlap.  The byte offsets code*4 come
-// from two shifted copies of each 32-bit word: byte b of (w >> 2) holds the
-// high nibble of byte b at bits 2..5, byte b of (w << 2) the low nibble, so
-// each offset is one byte-select AND.
-__device__ __forceinline__ void nf4_gather32(const uint4 pk, const float* cb, float* cw) {
+// (byte B of x) << 3 in one instruction (a byte-select shift), written as
+// asm for the same reason as byte_and_3c.
+template <int B>
+__device__ __forceinline__ uint32_t byte_shl3(uint32_t x) {
+    uint32_t r;
+    if constexpr (B == 0) {
+        asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
+            : "=v"(r) : "v"(3u), "v"(x));
+    } else if constexpr (B == 1) {
+        asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1"
+            : "=v"(r) : "v"(3u), "v"(x));
+    } else if constexpr (B == 2) {
+        asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2"
+            : "=v"(r) : "v"(3u), "v"(x));
+    } else {
+        asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3"
+            : "=v"(r) : "v"(3u), "v"(x));
+    }
+    return r;
+}
+
+// Codebook values of the 32 codes of one chunk, gathered from the LDS pair
+// table before any arithmetic so the lookups overlap.  Entry e of the table
+// holds (code[e >> 4], code[e & 15]), the values of both nibbles of byte e
+// (even element in the high nibble), so each byte costs one byte-select
+// shift (its offset e * 8) and one 8-byte LDS read.
+__device__ __forceinline__ void nf4_gather32(const uint4 pk, const float* pairs, float* cw) {
     const uint32_t w[4] = {pk.x, pk.y, pk.z, pk.w};
-    const char* base = reinterpret_cast<const char*>(cb);
+    const char* base = reinterpret_cast<const char*>(pairs);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t hi4 = w[i] >> 2;
-        const uint32_t lo4 = w[i] << 2;
-        cw[8 * i + 0] = *reinterpret_cast<const float*>(base + byte_and_3c<0>(hi4));
-        cw[8 * i + 1] = *reinterpret_cast<const float*>(base + byte_and_3c<0>(lo4));
-        cw[8 * i + 2] = *reinterpret_cast<const float*>(base + byte_and_3c<1>(hi4));
-        cw[8 * i + 3] = *reinterpret_cast<const float*>(base + byte_and_3c<1>(lo4));
-        cw[8 * i + 4] = *reinterpret_cast<const float*>(base + byte_and_3c<2>(hi4));
-        cw[8 * i + 5] = *reinterpret_cast<const float*>(base + byte_and_3c<2>(lo4));
-        cw[8 * i + 6] = *reinterpret_cast<const float*>(base + byte_and_3c<3>(hi4));
-        cw[8 * i + 7] = *reinterpret_cast<const float*>(base + byte_and_3c<3>(lo4));
+        const float2 p0 = *reinterpret_cast<const float2*>(base + byte_shl3<0>(w[i]));
+        const float2 p1 = *reinterpret_cast<const float2*>(base + byte_shl3<1>(w[i]));
+        const float2 p2 = *reinterpret_cast<const float2*>(base + byte_shl3<2>(w[i]));
+        const float2 p3 = *reinterpret_cast<const float2*>(base + byte_shl3<3>(w[i]));
+        cw[8 * i + 0] = p0.x;
+        cw[8 * i + 1] = p0.y;
+        cw[8 * i + 2] = p1.x;
+        cw[8 * i + 3] = p1.y;
+        cw[8 * i + 4] = p2.x;
+        cw[8 * i + 5] = p2.y;
+        cw[8 * i + 6] = p3.x;
+        cw[8 * i + 7] = p3.y;
     }
 }
 
 // Dot of one 32-element chunk with x[0..31] (already in fp32), before the
-// absmax multiply.  cb points at the codebook (LDS copy).
-__device__ __forceinline__ float nf4_chunk_dot_raw(const uint4 pk, const float* x, const float* cb) {
+// absmax multiply.  pairs points at the LDS pair table (block_pair_table_lds).
+__device__ __forceinline__ float nf4_chunk_dot_raw(const uint4 pk, const float* x, const float* pairs) {
     float cw[32];
-    nf4_gather32(pk, cb, cw);
+    nf4_gather32(pk, pairs, cw);
     float a[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -310,6 +333,18 @@ __device__ __forceinline__ float nf4_code_value(int i) {
 __device__ __forceinline__ void block_codebook_lds(float* cb) {
     if (threadIdx.x < 16) {
         cb[threadIdx.x] = nf4_code_value(static_cast<int>(threadIdx.x));
+    }
+}
+
+// Entries of the byte pair table: one per byte value, 8 bytes each.
+constexpr int kNf4PairEntries = 256;
+
+// Block-shared LDS pair table (see nf4_gather32): entry e = (code[e >> 4],
+// code[e & 15]), written by the block's threads from immediates; published by
+// the caller's block barrier like the codebook.
+__device__ __forceinline__ void block_pair_table_lds(float* pairs) {
+    for (int e = static_cast<int>(threadIdx.x); e < kNf4PairEntries; e += static_cast<int>(blockDim.x)) {
+        reinterpret_cast<float2*>(pairs)[e] = make_float2(nf4_code_value(e >> 4), nf4_code_value(e & 15));
     }
 }
 

@@ -188,7 +188,7 @@ __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs 
     // normalises a quarter of the vector, through LDS)
     constexpr bool kCoop = MODE != RowMode::kGemv;
     static_assert(!kCoop || kRowsThreads == 256, "four waves share the norm");
-    __shared__ float cb[16];
+    __shared__ __attribute__((aligned(16))) float cb[2 * kNf4PairEntries];
     __shared__ __attribute__((aligned(16))) uint16_t s_xa[ATTN ? 2048 : 8];
     __shared__ float s_ss[4];
     __shared__ __attribute__((aligned(16))) float s_xn[kCoop ? 64 * kNormPitch : 4];
@@ -343,7 +343,7 @@ __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs 
             s_ss[wave] = acc;
         }
     }
-    block_codebook_lds(cb);
+    block_pair_table_lds(cb);
     __syncthreads();
     if constexpr (ATTN) {
         if (merged) {
@@ -443,7 +443,7 @@ __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs 
 template <typename T, int NCHUNK, int R>
 __global__ __launch_bounds__(64 * ((NCHUNK + 63) / 64)) void nf4_down_kernel(Nf4DownArgs a) {
     constexpr int W = (NCHUNK + 63) / 64;
-    __shared__ float cb[16];
+    __shared__ __attribute__((aligned(16))) float cb[2 * kNf4PairEntries];
     __shared__ float red[R][W];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -477,7 +477,7 @@ __global__ __launch_bounds__(64 * ((NCHUNK + 63) / 64)) void nf4_down_kernel(Nf4
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    block_codebook_lds(cb);
+    block_pair_table_lds(cb);
     __syncthreads();
     float xv[32];
 #pragma unroll

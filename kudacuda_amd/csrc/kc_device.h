@@ -143,11 +143,17 @@ __device__ __forceinline__ float group16_sum(float v) {
     return v;
 }
 
-// Butterfly over the wave: partner distance 32, 16 (cross-row shuffles), then
-// the in-row stages 8..1.  Every lane ends with the same value.
+// Butterfly over the wave: partner distance 32, 16 (cross-row stages), then
+// the in-row stages 8..1.  Every lane ends with the same value.  The cross-row
+// stages use the lane-swap instructions on two copies of v: afterwards every
+// lane holds the pair {v[l], v[l ^ d]} (one value in each result), and their
+// sum is the stage's v[l] + v[l ^ d] (IEEE addition is commutative).  Call
+// with the whole wave active.
 __device__ __forceinline__ float wave_sum(float v) {
-    v += __shfl_xor(v, 32, 64);
-    v += __shfl_xor(v, 16, 64);
+    const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
+    const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
     return group16_sum(v);
 }
 
@@ -241,7 +247,7 @@ __device__ __forceinline__ void nf4_gather32(const uint4 pk, const float* pairs,
 }
 
 // Dot of one 32-element chunk with x[0..31] (already in fp32), before the
-// absmax multiply.  pairs points at the LDS pair table (block_pair_table_lds).
+// absmax multiply.  pairs points at the LDS copy of the pair table.
 __device__ __forceinline__ float nf4_chunk_dot_raw(const uint4 pk, const float* x, const float* pairs) {
     float cw[32];
     nf4_gather32(pk, pairs, cw);
@@ -339,12 +345,39 @@ __device__ __forceinline__ void block_codebook_lds(float* cb) {
 // Entries of the byte pair table: one per byte value, 8 bytes each.
 constexpr int kNf4PairEntries = 256;
 
-// Block-shared LDS pair table (see nf4_gather32): entry e = (code[e >> 4],
-// code[e & 15]), written by the block's threads from immediates; published by
-// the caller's block barrier like the codebook.
-__device__ __forceinline__ void block_pair_table_lds(float* pairs) {
-    for (int e = static_cast<int>(threadIdx.x); e < kNf4PairEntries; e += static_cast<int>(blockDim.x)) {
-        reinterpret_cast<float2*>(pairs)[e] = make_float2(nf4_code_value(e >> 4), nf4_code_value(e & 15));
+// The byte pair table (see nf4_gather32), entry e = (code[e >> 4],
+// code[e & 15]), built at compile time into the code object.
+struct Nf4PairTable {
+    float v[2 * kNf4PairEntries];
+};
+constexpr Nf4PairTable nf4_make_pair_table() {
+    constexpr float cb[16] = {
+        -0x1.000000p+0f, -0x1.647362p-1f, -0x1.0cd660p-1f, -0x1.946540p-2f,
+        -0x1.23449ap-2f, -0x1.7a6a7ep-3f, -0x1.74f0e2p-4f, 0x0.0p+0f,
+        0x1.45f5fep-4f,  0x1.4995c6p-3f,  0x1.f809bap-3f,  0x1.5a0674p-2f,
+        0x1.c34970p-2f,  0x1.200f56p-1f,  0x1.722766p-1f,  0x1.000000p+0f,
+    };
+    Nf4PairTable t{};
+    for (int e = 0; e < kNf4PairEntries; ++e) {
+        t.v[2 * e] = cb[e >> 4];
+        t.v[2 * e + 1] = cb[e & 15];
+    }
+    return t;
+}
+__device__ constexpr Nf4PairTable kNf4PairTable = nf4_make_pair_table();
+
+// Block-shared LDS copy of the pair table, in two steps so the global load
+// can be issued before the kernel's weight loads (a wait for it then does not
+// wait for them): pair_entry_fetch() returns this thread's entry (threads past
+// the table re-read entry t & 255), pair_entry_store() writes it (threads
+// below 256 only; blocks have at least 256 threads).  The caller publishes the
+// table with a block barrier.
+__device__ __forceinline__ float2 pair_entry_fetch() {
+    return reinterpret_cast<const float2*>(kNf4PairTable.v)[threadIdx.x & (kNf4PairEntries - 1)];
+}
+__device__ __forceinline__ void pair_entry_store(float* pairs, float2 e) {
+    if (threadIdx.x < kNf4PairEntries) {
+        reinterpret_cast<float2*>(pairs)[threadIdx.x] = e;
     }
 }
 

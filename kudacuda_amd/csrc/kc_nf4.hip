@@ -134,9 +134,7 @@ __device__ __forceinline__ void row_epilogue(const Nf4RowsArgs& a, const RowPair
             a.out[0][r] = T::store(v);
         }
     } else if constexpr (MODE == RowMode::kSwiGlu) {
-        if (lane == 0) {
-            a.out[0][cur.r0] = T::store(silu_fixed(d0) * d1);
-        }
+        // the row kernel stores SwiGLU outputs itself, one lane per task
     } else {
         if (lane == 0) {
             const int m = cur.m0;
@@ -197,6 +195,8 @@ __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs 
     const int64_t waves_per_block = kRowsThreads / 64;
     const int64_t nwaves = static_cast<int64_t>(gridDim.x) * waves_per_block;
     const int64_t first = static_cast<int64_t>(blockIdx.x) * waves_per_block + wave;
+    static_assert(kRowsThreads >= kNf4PairEntries, "one pair-table entry per thread");
+    const float2 pair_entry = pair_entry_fetch();
 
     int64_t pos = 0;
     if constexpr (MODE == RowMode::kQkvRope) {
@@ -343,7 +343,7 @@ __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs 
             s_ss[wave] = acc;
         }
     }
-    block_pair_table_lds(cb);
+    pair_entry_store(cb, pair_entry);
     __syncthreads();
     if constexpr (ATTN) {
         if (merged) {
@@ -401,6 +401,10 @@ __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs 
         }
     }
 
+    // kSwiGlu: lane i keeps task i's gate and up sums, and the epilogue runs
+    // once for the wave (lanes 0 .. TPW-1)
+    float gate = 0.0f, up = 0.0f;
+    int64_t out_row = tasks[0].r0;
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
         const float d0 = wave_sum(nf4_chunk_dot_raw(pk[i][0], xn, cb) * am[i][0]);
@@ -408,8 +412,17 @@ __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs 
         if (tasks[i].has1) {
             d1 = wave_sum(nf4_chunk_dot_raw(pk[i][1], xn, cb) * am[i][1]);
         }
-        if (first + i * nwaves < ntasks) {
+        if constexpr (MODE == RowMode::kSwiGlu) {
+            gate = lane == i ? d0 : gate;
+            up = lane == i ? d1 : up;
+            out_row = lane == i ? tasks[i].r0 : out_row;
+        } else if (first + i * nwaves < ntasks) {
             row_epilogue<T, MODE>(a, tasks[i], epi[i], d0, d1, lane, pos);
+        }
+    }
+    if constexpr (MODE == RowMode::kSwiGlu) {
+        if (lane < TPW && first + lane * nwaves < ntasks) {
+            a.out[0][out_row] = T::store(silu_fixed(gate) * up);
         }
     }
 
@@ -454,6 +467,8 @@ __global__ __launch_bounds__(64 * ((NCHUNK + 63) / 64)) void nf4_down_kernel(Nf4
     const int64_t row_blocks = NCHUNK / 2;
     const int64_t rbase = static_cast<int64_t>(blockIdx.x) * R;
     const int64_t last_row = a.rows - 1;
+    static_assert(64 * W >= kNf4PairEntries, "one pair-table entry per thread");
+    const float2 pair_entry = pair_entry_fetch();
 
     uint4 xr[4];
     const uint4* src = reinterpret_cast<const uint4*>(a.x) + static_cast<int64_t>(cc) * 4;
@@ -477,7 +492,7 @@ __global__ __launch_bounds__(64 * ((NCHUNK + 63) / 64)) void nf4_down_kernel(Nf4
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    block_pair_table_lds(cb);
+    pair_entry_store(cb, pair_entry);
     __syncthreads();
     float xv[32];
 #pragma unroll

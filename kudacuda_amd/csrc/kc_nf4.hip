@@ -261,13 +261,23 @@ __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs 
         tasks[i] = map_task<MODE>(a, t < ntasks ? t : ntasks - 1);
         epi[i] = fetch_epilogue<T, MODE>(a, tasks[i], lane, pos);
     }
+    // Rows of the first kEarly tasks are requested up front, the rest one task
+    // at a time after the previous task's dots.  A wave whose load cannot be
+    // issued yet (the CU's memory queue is full while the launch's weights
+    // stream in) stalls in order, so gate/up waves that queue all their rows
+    // at once sit idle until the stream drains and then all compute together;
+    // issuing task i + 1 after task i's dots overlaps the two phases.
     uint4 pk[TPW][2];
     float am[TPW][2];
-#pragma unroll
-    for (int i = 0; i < TPW; ++i) {
-        __builtin_amdgcn_sched_barrier(0);
+    constexpr int kEarly = MODE == RowMode::kSwiGlu ? 1 : TPW;
+    auto fetch_task = [&](int i) {
         fetch_row(a, tasks[i].m0, tasks[i].r0, lane, pk[i][0], am[i][0]);
         fetch_row(a, tasks[i].m1, tasks[i].has1 ? tasks[i].r1 : tasks[i].r0, lane, pk[i][1], am[i][1]);
+    };
+#pragma unroll
+    for (int i = 0; i < kEarly; ++i) {
+        __builtin_amdgcn_sched_barrier(0);
+        fetch_task(i);
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -407,6 +417,11 @@ __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs 
     int64_t out_row = tasks[0].r0;
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
+        if (i >= kEarly) {
+            __builtin_amdgcn_sched_barrier(0);
+            fetch_task(i);
+            __builtin_amdgcn_sched_barrier(0);
+        }
         const float d0 = wave_sum(nf4_chunk_dot_raw(pk[i][0], xn, cb) * am[i][0]);
         float d1 = 0.0f;
         if (tasks[i].has1) {

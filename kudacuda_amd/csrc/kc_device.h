@@ -157,6 +157,22 @@ __device__ __forceinline__ float wave_sum(float v) {
     return group16_sum(v);
 }
 
+// Two butterflies at the price of one: the first lane swap takes a's upper
+// half and b's lower half, so after its sum lanes 0..31 hold a's distance-32
+// stage and lanes 32..63 b's; the remaining stages pair lanes inside each half
+// only.  A last swap hands out {sum(a), sum(b)} to every lane.  Each row's
+// additions are the pairs and order of wave_sum, so the sums are identical to
+// wave_sum(a) and wave_sum(b).  Call with the whole wave active.
+__device__ __forceinline__ float2 wave_sum2(float a, float b) {
+    const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    float v = __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
+    const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
+    v = group16_sum(v);
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // -------------------------------------------------- cross-block exchange
 // Blocks of one launch that hand results to a "last block" (ticket pattern)
 // exchange only a few words.  A device-scope fence would write back and

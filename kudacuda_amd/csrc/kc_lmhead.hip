@@ -138,9 +138,12 @@ __global__ __launch_bounds__(kLmThreads) void lm_head_kernel(LmHeadArgs a) {
                 // keep slot i's refill ahead of slot i+1's dot
                 __builtin_amdgcn_sched_barrier(0);
             }
+            static_assert(kRing % 2 == 0, "rows reduced in pairs");
 #pragma unroll
-            for (int i = 0; i < kRing; ++i) {
-                sum[i] = wave_sum(sum[i]);
+            for (int i = 0; i < kRing; i += 2) {
+                const float2 s2 = wave_sum2(sum[i], sum[i + 1]);
+                sum[i] = s2.x;
+                sum[i + 1] = s2.y;
             }
             // lane i (< kRing) stores slot i's logit: one store per pass
             uint16_t lane_lb = 0;

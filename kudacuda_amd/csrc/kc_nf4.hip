@@ -422,10 +422,14 @@ __global__ __launch_bounds__(kRowsThreads) void nf4_rows2048_kernel(Nf4RowsArgs 
             fetch_task(i);
             __builtin_amdgcn_sched_barrier(0);
         }
-        const float d0 = wave_sum(nf4_chunk_dot_raw(pk[i][0], xn, cb) * am[i][0]);
-        float d1 = 0.0f;
+        float d0, d1 = 0.0f;
         if (tasks[i].has1) {
-            d1 = wave_sum(nf4_chunk_dot_raw(pk[i][1], xn, cb) * am[i][1]);
+            const float2 d = wave_sum2(nf4_chunk_dot_raw(pk[i][0], xn, cb) * am[i][0],
+                                       nf4_chunk_dot_raw(pk[i][1], xn, cb) * am[i][1]);
+            d0 = d.x;
+            d1 = d.y;
+        } else {
+            d0 = wave_sum(nf4_chunk_dot_raw(pk[i][0], xn, cb) * am[i][0]);
         }
         if constexpr (MODE == RowMode::kSwiGlu) {
             gate = lane == i ? d0 : gate;
@@ -515,12 +519,15 @@ __global__ __launch_bounds__(64 * ((NCHUNK + 63) / 64)) void nf4_down_kernel(Nf4
         unpack8<T>(xr[i], xv + 8 * i);
     }
 
+    static_assert(R % 2 == 0, "rows reduced in pairs");
 #pragma unroll
-    for (int i = 0; i < R; ++i) {
-        float p = nf4_chunk_dot_raw(pk[i], xv, cb) * am[i];
-        p = wave_sum(valid ? p : 0.0f);
+    for (int i = 0; i < R; i += 2) {
+        const float p0 = nf4_chunk_dot_raw(pk[i], xv, cb) * am[i];
+        const float p1 = nf4_chunk_dot_raw(pk[i + 1], xv, cb) * am[i + 1];
+        const float2 p = wave_sum2(valid ? p0 : 0.0f, valid ? p1 : 0.0f);
         if (lane == 0) {
-            red[i][wave] = p;
+            red[i][wave] = p.x;
+            red[i + 1][wave] = p.y;
         }
     }
     __syncthreads();

@@ -7,12 +7,16 @@
 //    of chunk l with one 128-bit load, so a wave load is one contiguous
 //    1 KiB row (fully coalesced) and the lane's 32 activations stay in
 //    registers for every row the wave visits;
-//  * the 16-entry fp32 codebook lives in LDS (16 distinct banks: a lookup is
-//    never a bank conflict);
-//  * the RMSNorm is recomputed per wave from the 4 KiB input (an L2 hit after
-//    the first wave) so no block barrier or separate norm launch is needed;
-//  * each wave prefetches its next task's rows before reducing the current
-//    one, keeping two rows per lane in flight.
+//  * codes are looked up in a block-shared LDS table of code pairs (one
+//    8-byte entry per byte value), one byte-select shift per byte;
+//  * the RMSNorm is computed inside the consumer kernel: the 4 waves of a
+//    block share it (a quarter each, through LDS), so no separate norm
+//    launch is needed;
+//  * loads are issued in dependency order (activations, epilogue operands,
+//    rows), and gate/up requests its second task's rows only after its first
+//    task's dots (a wave stalled on a full memory queue stops in order);
+//  * reductions are wave64 butterflies on lane-swap and DPP instructions,
+//    two rows per chain.
 // Semantics follow the reference's tiled NF4 kernels
 // (kernels/common/nf4_tiled_gemv.cuh:61-168: norm in fp32, dot in fp32,
 // bias added in fp32 before the single output rounding) and its SwiGLU

@@ -685,7 +685,7 @@ hipError_t launch_nf4_rows2048(RowMode mode, Act act, const Nf4RowsArgs& a, hipS
 
 hipError_t launch_nf4_down11008(Act act, const Nf4DownArgs& a, hipStream_t stream) {
     constexpr int kChunks = 11008 / 32;
-    constexpr int kRows = 2;  // 1024 blocks of 6 waves: measured faster than 4 or 8 rows per block
+    constexpr int kRows = 4;  // 512 blocks of 6 waves: measured faster than 2 or 8 rows per block
     constexpr int kThreads = 64 * ((kChunks + 63) / 64);
     if (a.rows <= 0) {
         return hipSuccess;

@@ -195,29 +195,8 @@ __device__ __forceinline__ float load_agent(const float* p) {
 __device__ __forceinline__ void wait_own_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // ------------------------------------------------------------------ NF4 dots
-// (byte B of x) & 0x3c in one instruction (a byte-select AND), written as asm:
-// the compiler folds a byte-select AND back into a shift and an AND.
-template <int B>
-__device__ __forceinline__ uint32_t byte_and_3c(uint32_t x) {
-    uint32_t r;
-    if constexpr (B == 0) {
-        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
-            : "=v"(r) : "v"(0x3cu), "v"(x));
-    } else if constexpr (B == 1) {
-        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1"
-            : "=v"(r) : "v"(0x3cu), "v"(x));
-    } else if constexpr (B == 2) {
-        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2"
-            : "=v"(r) : "v"(0x3cu), "v"(x));
-    } else {
-        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3"
-            : "=v"(r) : "v"(0x3cu), "v"(x));
-    }
-    return r;
-}
-
 // (byte B of x) << 3 in one instruction (a byte-select shift), written as
-// asm for the same reason as byte_and_3c.
+// asm: the compiler folds a byte-select operand back into a shift and an AND.
 template <int B>
 __device__ __forceinline__ uint32_t byte_shl3(uint32_t x) {
     uint32_t r;
@@ -331,33 +310,6 @@ __device__ __forceinline__ void load_norm_x2048(const uint16_t* __restrict__ x,
     }
 }
 
-// Codebook entry i (0..15) selected from immediates, so building the LDS copy
-// costs no memory round trip at kernel start.
-__device__ __forceinline__ float nf4_code_value(int i) {
-    constexpr float cb[16] = {
-        -0x1.000000p+0f, -0x1.647362p-1f, -0x1.0cd660p-1f, -0x1.946540p-2f,
-        -0x1.23449ap-2f, -0x1.7a6a7ep-3f, -0x1.74f0e2p-4f, 0x0.0p+0f,
-        0x1.45f5fep-4f,  0x1.4995c6p-3f,  0x1.f809bap-3f,  0x1.5a0674p-2f,
-        0x1.c34970p-2f,  0x1.200f56p-1f,  0x1.722766p-1f,  0x1.000000p+0f,
-    };
-    float v = cb[0];
-#pragma unroll
-    for (int k = 1; k < 16; ++k) {
-        v = i == k ? cb[k] : v;
-    }
-    return v;
-}
-
-// Block-shared LDS copy of the codebook at a fixed LDS address (so every
-// lookup's base folds into the ds_read offset): threads 0..15 write it; the
-// caller publishes it with a block barrier placed after its global loads are
-// issued, so the barrier overlaps memory latency.
-__device__ __forceinline__ void block_codebook_lds(float* cb) {
-    if (threadIdx.x < 16) {
-        cb[threadIdx.x] = nf4_code_value(static_cast<int>(threadIdx.x));
-    }
-}
-
 // Entries of the byte pair table: one per byte value, 8 bytes each.
 constexpr int kNf4PairEntries = 256;
 
@@ -367,16 +319,10 @@ struct Nf4PairTable {
     float v[2 * kNf4PairEntries];
 };
 constexpr Nf4PairTable nf4_make_pair_table() {
-    constexpr float cb[16] = {
-        -0x1.000000p+0f, -0x1.647362p-1f, -0x1.0cd660p-1f, -0x1.946540p-2f,
-        -0x1.23449ap-2f, -0x1.7a6a7ep-3f, -0x1.74f0e2p-4f, 0x0.0p+0f,
-        0x1.45f5fep-4f,  0x1.4995c6p-3f,  0x1.f809bap-3f,  0x1.5a0674p-2f,
-        0x1.c34970p-2f,  0x1.200f56p-1f,  0x1.722766p-1f,  0x1.000000p+0f,
-    };
     Nf4PairTable t{};
     for (int e = 0; e < kNf4PairEntries; ++e) {
-        t.v[2 * e] = cb[e >> 4];
-        t.v[2 * e + 1] = cb[e & 15];
+        t.v[2 * e] = kNf4Codebook[e >> 4];
+        t.v[2 * e + 1] = kNf4Codebook[e & 15];
     }
     return t;
 }

@@ -56,27 +56,22 @@ __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast
 // 8 codes of one 32-bit word (byte b: element 2b in the high nibble, 2b+1 in
 // the low nibble) times absmax, each rounded to bf16 (round to nearest even,
 // v_cvt_pk_bf16_f32; the products are finite); element j lands in slot j.
-// The codebook byte offsets (4 * code) come from two shifted copies of the
-// word: byte b of (word >> 2) holds the high nibble of byte b at bits 2..5,
-// byte b of (word << 2) the low nibble, so each offset is one byte-select AND
-// (byte_and_3c).
+// Both codes of byte b come from one 8-byte read of the LDS pair table at
+// offset (byte b) * 8, a byte-select shift (byte_shl3).
 template <int B>
-__device__ __forceinline__ void dequant_byte(bf16x8& v, uint32_t hi4, uint32_t lo4, float am, const char* base) {
-    const uint32_t oh = byte_and_3c<B>(hi4);
-    const uint32_t ol = byte_and_3c<B>(lo4);
-    v[2 * B] = static_cast<__bf16>(*reinterpret_cast<const float*>(base + oh) * am);
-    v[2 * B + 1] = static_cast<__bf16>(*reinterpret_cast<const float*>(base + ol) * am);
+__device__ __forceinline__ void dequant_byte(bf16x8& v, uint32_t word, float am, const char* base) {
+    const float2 p = *reinterpret_cast<const float2*>(base + byte_shl3<B>(word));
+    v[2 * B] = static_cast<__bf16>(p.x * am);
+    v[2 * B + 1] = static_cast<__bf16>(p.y * am);
 }
 
-__device__ __forceinline__ bf16x8 dequant8_bf16(uint32_t word, float am, const float* cb) {
-    const uint32_t hi4 = word >> 2;
-    const uint32_t lo4 = word << 2;
-    const char* base = reinterpret_cast<const char*>(cb);
+__device__ __forceinline__ bf16x8 dequant8_bf16(uint32_t word, float am, const float* pairs) {
+    const char* base = reinterpret_cast<const char*>(pairs);
     bf16x8 v;
-    dequant_byte<0>(v, hi4, lo4, am, base);
-    dequant_byte<1>(v, hi4, lo4, am, base);
-    dequant_byte<2>(v, hi4, lo4, am, base);
-    dequant_byte<3>(v, hi4, lo4, am, base);
+    dequant_byte<0>(v, word, am, base);
+    dequant_byte<1>(v, word, am, base);
+    dequant_byte<2>(v, word, am, base);
+    dequant_byte<3>(v, word, am, base);
     return v;
 }
 
@@ -142,8 +137,10 @@ template <GemmEpi EPI, int NT>
 __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(Nf4GemmArgs a) {
     constexpr bool kSw = EPI == GemmEpi::kSwiGlu;
     constexpr int kBlockRows = kSw ? kRowsPerBlock / 2 : kRowsPerBlock;  // output rows of the block
-    __shared__ float cb[16];
+    __shared__ __attribute__((aligned(16))) float cb[2 * kNf4PairEntries];
     __shared__ __attribute__((aligned(16))) uint8_t s_x[2][16 * NT * kXPitch];
+    static_assert(kGemmThreads >= kNf4PairEntries, "one pair-table entry per thread");
+    const float2 pair_entry = pair_entry_fetch();  // first request: its wait below waits for nothing else
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -177,7 +174,6 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(Nf4GemmArgs a) {
         xrow[j] = a.x + static_cast<int64_t>(m) * K;
     }
     const int xcol = 8 * (tid % 16);
-    block_codebook_lds(cb);
 
     floatx4 acc[NT];
 #pragma unroll
@@ -199,6 +195,7 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(Nf4GemmArgs a) {
     u32x16 x2;
     u32x8 w2;
     x_stage<NT>(sx, x0, tid);
+    pair_entry_store(cb, pair_entry);
     __syncthreads();
     int buf = 0;
     int64_t kw = k_begin;

@@ -7,12 +7,12 @@
 // group holds dims [8li, 8li+8) of all 8 query heads.  Two paths, chosen per
 // launch from kv_len L (uniform over the grid):
 //
-// Flat path (L <= flat_max, at most 16 splits): split s owns tokens
+// Flat path (L <= flat_max, at most 32 splits): split s owns tokens
 // [32s, min(32s+32, L)), one per group.  Each group forms its token's 8 head
 // scores (8-dim partial dots and the 16-lane butterfly below), the block takes
 // the per-head max M over the split, weights w_t = exp2(s_t - M), sum
 // l = w_0 + w_1 + ..., and acc[d] = sum_t w_t v_t[d] in token order, with the
-// V rows staged in LDS.  Short caches thus spread over up to 32 CUs instead of
+// V rows staged in LDS.  Short caches thus spread over up to 64 CUs instead of
 // running a long per-group chain on 2.
 //
 // Round path (longer L): split s owns tokens [s*C, min(s*C+C, L)), C = 128
@@ -69,10 +69,10 @@ constexpr int kHeadsPerGroup = 8;
 constexpr int kDim = 128;
 constexpr int kPartialStride = kGqaPartialStride;
 static_assert(kPartialStride == 2 + kDim, "partial layout: max, sum, acc[128]");
-constexpr int kInKernelSplits = 16;
+constexpr int kInKernelSplits = 32;
 constexpr int kFlatTokens = kGqaFlatTokens;  // flat path: one token per group, one round per split
 static_assert(kFlatTokens == kGroups, "flat path: one token per 16-lane group");
-constexpr int kFlatSplits = 16;
+constexpr int kFlatSplits = 32;
 constexpr int kMergeMaxSplits = 1024;
 constexpr int kMergeDims = 16;              // dims per merge block
 constexpr int kSlot = 40;                   // per-group LDS exchange: 32 scores + 8 rescales
@@ -101,6 +101,46 @@ __device__ __forceinline__ void load_rows(const uint16_t* kbase, const uint16_t*
 }
 
 __device__ __forceinline__ int clamp4(int64_t n) { return static_cast<int>(n < 0 ? 0 : (n > 4 ? 4 : n)); }
+
+// In-kernel merge of the first nsplit (<= N) split partials of KV head g
+// (the last block of the head runs it): every thread owns two (head, dim)
+// outputs, loads every split's max, sum and accumulator element for them
+// (agent-scope loads: the partials come from other blocks of this launch),
+// and sums in split order with weights exp2(m_s - M).
+template <typename T, int N>
+__device__ __forceinline__ void ticket_merge(const GqaArgs& a, const float* part, int g, int nsplit) {
+#pragma unroll 1
+    for (int k = 0; k < 2; ++k) {
+        const int idx = threadIdx.x + k * kGqaThreads;
+        const int hl = idx / kDim;
+        const int d = idx % kDim;
+        const float* src = part + (g * kHeadsPerGroup + hl) * a.max_splits * kPartialStride;
+        float mv[N], lv[N], vv[N];
+#pragma unroll
+        for (int x = 0; x < N; ++x) {
+            const bool live = x < nsplit;
+            mv[x] = live ? load_agent(src + x * kPartialStride) : kNegInf;
+            lv[x] = live ? load_agent(src + x * kPartialStride + 1) : 0.0f;
+            vv[x] = live ? load_agent(src + x * kPartialStride + 2 + d) : 0.0f;
+        }
+        float M = kNegInf;
+#pragma unroll
+        for (int x = 0; x < N; ++x) {
+            M = fmaxf(M, mv[x]);
+        }
+        float lt = 0.0f;
+        float o = 0.0f;
+#pragma unroll
+        for (int x = 0; x < N; ++x) {
+            if (x < nsplit) {
+                const float w = exp2_fixed(mv[x] - M);
+                lt = fmaf(lv[x], w, lt);
+                o = fmaf(vv[x], w, o);
+            }
+        }
+        a.out[(g * kHeadsPerGroup + hl) * kDim + d] = T::store(o / lt);
+    }
+}
 
 template <typename T>
 __global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a) {
@@ -525,36 +565,13 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a) {
     // One pass: every thread issues all the loads it needs (the split maxima
     // and sums of its head and its element of every split's accumulator),
     // then forms the weights exp2(m_s - M) itself and sums in split order.
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        const int idx = threadIdx.x + k * kGqaThreads;
-        const int hl = idx / kDim;
-        const int d = idx % kDim;
-        const float* src = part + (g * kHeadsPerGroup + hl) * a.max_splits * kPartialStride;
-        float mv[kInKernelSplits], lv[kInKernelSplits], vv[kInKernelSplits];
-#pragma unroll
-        for (int x = 0; x < kInKernelSplits; ++x) {
-            const bool live = x < nsplit;
-            mv[x] = live ? load_agent(src + x * kPartialStride) : kNegInf;
-            lv[x] = live ? load_agent(src + x * kPartialStride + 1) : 0.0f;
-            vv[x] = live ? load_agent(src + x * kPartialStride + 2 + d) : 0.0f;
-        }
-        float M = kNegInf;
-#pragma unroll
-        for (int x = 0; x < kInKernelSplits; ++x) {
-            M = fmaxf(M, mv[x]);
-        }
-        float lt = 0.0f;
-        float o = 0.0f;
-#pragma unroll
-        for (int x = 0; x < kInKernelSplits; ++x) {
-            if (x < nsplit) {
-                const float w = exp2_fixed(mv[x] - M);
-                lt = fmaf(lv[x], w, lt);
-                o = fmaf(vv[x], w, o);
-            }
-        }
-        a.out[(g * kHeadsPerGroup + hl) * kDim + d] = T::store(o / lt);
+    // Up to 16 splits use 16-wide register arrays, more the 32-wide ones
+    // (same operations in the same order; the narrow form keeps the common
+    // short merges as cheap as before).
+    if (nsplit <= kInKernelSplits / 2) {
+        ticket_merge<T, kInKernelSplits / 2>(a, part, g, static_cast<int>(nsplit));
+    } else {
+        ticket_merge<T, kInKernelSplits>(a, part, g, static_cast<int>(nsplit));
     }
 }
 
@@ -648,9 +665,10 @@ __global__ __launch_bounds__(256) void gqa_merge_kernel(GqaArgs a) {
 
 }  // namespace
 
-// Split rule (measured on MI355X): flat path up to 16 x 32 tokens; round
-// path with 128-token splits up to 8192 tokens (more blocks at mid lengths:
-// 1024 tokens 15.9 -> 13.7 us, 8192 tokens 17.7 -> 15.3 us), 256-token splits
+// Split rule (measured on MI355X): flat path up to 32 x 32 tokens (585-1024
+// tokens: 13.4 -> 8.9 us against 128-token round splits); round path with
+// 128-token splits up to 8192 tokens (more blocks at mid lengths: 8192 tokens
+// 17.7 -> 15.3 us against 256-token splits), 256-token splits
 // beyond (at 32768 tokens 256 splits of 128 cost more in the merge than they
 // save: 30.4 vs 22.1 us).
 constexpr int64_t kMidMax = 8192;

@@ -351,7 +351,7 @@ hipError_t model_op(const Model& m, int op, int64_t layer, bool bookkeeping, hip
             a.defer_max = model_defer(a.max_splits);  // o_proj merges these
             // the rest by ticket: a merge kernel would be one more graph node
             // per layer even at the lengths that never need it
-            a.ticket_max = 16;
+            a.ticket_max = 32;
             a.qk_scale_log2 = static_cast<float>(1.0 / std::sqrt(128.0)) * kLog2e;
             return launch_gqa_decode(Act::kBf16, a, stream);
         }

@@ -384,7 +384,7 @@ KCO_API void kco_down11008(int act, const uint16_t* x, const uint8_t* w, const f
 
 /* Flat path: kv_len <= flat_max, GQA_GROUPS tokens per split (one per group),
  * at most GQA_FLAT_SPLITS splits. */
-#define GQA_FLAT_SPLITS 16
+#define GQA_FLAT_SPLITS 32
 
 /* tokens per split on the round path for a cache of `tokens` rows */
 KCO_API int64_t kco_gqa_chunk_for(int64_t tokens) { (void)tokens; return 2 * GQA_ROUND; }

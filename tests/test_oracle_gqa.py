@@ -91,11 +91,11 @@ def test_planted_wrong_group_mapping_fails():
 
 def test_split_plan_covers_every_regime():
     # (chunk, flat_max, mid_max, max_splits): flat path with 32-token splits up
-    # to 16 x 32 tokens (8 x 32 with the reference's 16 x 8 x 130 workspace),
+    # to 32 x 32 tokens (8 x 32 with the reference's 16 x 8 x 130 workspace),
     # round path with 128-token splits up to 8192 tokens, 256-token beyond
-    assert O.gqa_plan(2048) == (256, 512, 2048, 16)
-    assert O.gqa_plan(32768) == (256, 512, 8192, 128)
-    assert O.gqa_plan(65536) == (256, 512, 8192, 256)
+    assert O.gqa_plan(2048) == (256, 1024, 2048, 32)
+    assert O.gqa_plan(32768) == (256, 1024, 8192, 128)
+    assert O.gqa_plan(65536) == (256, 1024, 8192, 256)
     assert O.gqa_plan(100) == (256, 100, 100, 4)
     assert O.gqa_plan(512, split_limit=8) == (256, 256, 512, 8)
     assert O.gqa_plan(1) == (256, 1, 1, 1)

@@ -81,3 +81,21 @@ def test_generate_matches_oracle_tokens(small_pair):
     gpu, cpu = small_pair
     prompt = synthetic.prompt_ids(SEED + 2, 9, 4096)
     assert np.array_equal(gpu.generate(prompt, 24), cpu.generate(prompt, 24))
+
+
+@pytest.mark.parametrize("prompt_len,new,capacity", [(600, 24, 1024), (1030, 8, 2048)])
+def test_long_context_decode_matches_oracle(torch_gpu, native, prompt_len, new, capacity):
+    # Decode-step attention past the short-context regime: at 600+ cached
+    # tokens the flat path runs 19-20 splits of 32 tokens, more than o_proj
+    # merges, so the attention kernel's in-kernel merge of up to 32 splits
+    # runs; past 1024 tokens the round path's 128-token splits take over.
+    kw = dict(num_layers=2, vocab=4096, kv_capacity=capacity, token_capacity=capacity)
+    gpu = Qwen2Nf4Decoder.synthetic(native, torch_gpu, seed=SEED, **kw)
+    cpu = HostModel(SEED, **kw)
+    try:
+        prompt = synthetic.prompt_ids(SEED + 3, prompt_len, 4096)
+        assert np.array_equal(gpu.generate(prompt, new), cpu.generate(prompt, new))
+        assert np.array_equal(host(gpu.logits), cpu.logits)
+        assert np.array_equal(host(gpu.attn), cpu.attn)
+    finally:
+        gpu.close()

@@ -9,9 +9,9 @@
 //    registers for every row the wave visits;
 //  * codes are looked up in a block-shared LDS table of code pairs (one
 //    8-byte entry per byte value), one byte-select shift per byte;
-//  * the RMSNorm is computed inside the consumer kernel: the 4 waves of a
-//    block share it (a quarter each, through LDS), so no separate norm
-//    launch is needed;
+//  * the RMSNorm is computed inside the consumer kernel: waves 0..3 of a
+//    block each normalise a quarter into LDS and every wave of the block
+//    (4, or 12 in gate/up) reads it, so no separate norm launch is needed;
 //  * loads are issued in dependency order (activations, epilogue operands,
 //    rows), and gate/up requests its second task's rows only after its first
 //    task's dots (a wave stalled on a full memory queue stops in order);
@@ -191,8 +191,8 @@ template <typename T, RowMode MODE, int TPW, bool ATTN = false, int NTH = kRowsT
 __global__ __launch_bounds__(NTH) void nf4_rows2048_kernel(Nf4RowsArgs a, int64_t ntasks) {
     static_assert(!ATTN || MODE == RowMode::kGemv, "attention merge feeds the GEMV only");
     static_assert(!ATTN || kRowsThreads * 8 == 2048, "one thread per 8 merged outputs");
-    // kQkv / kQkvRope / kSwiGlu: the block's 4 waves share the RMSNorm (each
-    // normalises a quarter of the vector, through LDS)
+    // kQkv / kQkvRope / kSwiGlu: the block shares the RMSNorm (waves 0..3 each
+    // normalise a quarter of the vector into LDS, every wave reads it)
     constexpr bool kCoop = MODE != RowMode::kGemv;
     static_assert(!kCoop || (NTH >= 256 && NTH % 64 == 0), "waves 0..3 compute the shared norm");
     static_assert(!ATTN || NTH == kRowsThreads, "merge layout");

@@ -13,7 +13,8 @@
 // the per-head max M over the split, weights w_t = exp2(s_t - M), sum
 // l = w_0 + w_1 + ..., and acc[d] = sum_t w_t v_t[d] in token order, with the
 // V rows staged in LDS.  Short caches thus spread over up to 64 CUs instead of
-// running a long per-group chain on 2.
+// running a long per-group chain on 2.  Up to 2 * flat_max the same path runs
+// with two tokens per group (64-token splits, the same split count).
 //
 // Round path (longer L): split s owns tokens [s*C, min(s*C+C, L)), C = 128
 // up to mid_max and `chunk` (256) beyond, both chosen from L on the device.  Per
@@ -184,6 +185,7 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a) {
     if (s == 0) {
         load_rows(kbase, vbase, 4 * gi, a.capacity - 1, kA, vA);
     }
+
     const int64_t L = read_kv_len(a);
     const int64_t nsplit = split_count(a, L);
     if (s >= nsplit) {
@@ -275,6 +277,107 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a) {
 #pragma unroll 8
             for (int x = 0; x < nvalid; ++x) {
                 const float w = s_w[hl][x];
+                acc_f = fmaf(w, s_vf[x][dd], acc_f);
+                lsum = lsum + w;
+            }
+            av_out[half] = acc_f;
+            if (dd == 0) {
+                s_L[hl] = lsum;
+            }
+        }
+        __syncthreads();
+    } else if (L <= 2 * a.flat_max) {
+        // ---- flat path, two tokens per group (64-token splits): group gi
+        // scores tokens f0 + gi and f0 + 32 + gi with the dot and butterfly
+        // above, then the same block-wide softmax per head over the split's
+        // tokens and the weighted V sum in token order.  Its rows are
+        // requested here, after kv_len: the early requests are the one-token
+        // layout's (requesting both layouts up front costs every short
+        // length more than it saves here).
+        float (*s_vf)[kDim] = reinterpret_cast<float (*)[kDim]>(&s_acc[0][0][0]);
+        float (*s_sc)[2 * kGroups] = reinterpret_cast<float (*)[2 * kGroups]>(&s_x[0][0]);
+        float (*s_wt)[2 * kGroups] = s_sc + kHeadsPerGroup;
+        static_assert(2 * kHeadsPerGroup * 2 * kGroups <= kGroups * kSlot, "scores and weights fit the slots");
+        static_assert(2 * kGroups * kDim <= kGroups * (kHeadsPerGroup / 2) * kDim, "64 V rows fit the stage");
+        static_assert(kHeadsPerGroup * 2 * kGroups == kGqaThreads, "one thread per (head, token)");
+        const int64_t f0 = s * 2 * kFlatTokens;
+        const int nvalid = static_cast<int>(f0 + 2 * kFlatTokens < L ? 2 * kFlatTokens : L - f0);
+        uint4 k2[2], v2[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int64_t t = f0 + kFlatTokens * u + gi;
+            const int64_t tc = t < a.capacity ? t : a.capacity - 1;
+            k2[u] = *reinterpret_cast<const uint4*>(kbase + tc * kDim);
+            v2[u] = *reinterpret_cast<const uint4*>(vbase + tc * kDim);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            float kf[8], vf[8];
+            unpack8<T>(k2[u], kf);
+            unpack8<T>(v2[u], vf);
+            float dots[kHeadsPerGroup];
+#pragma unroll
+            for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
+                float t = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    t = fmaf(q[hl][j], kf[j], t);
+                }
+                dots[hl] = t;
+            }
+#pragma unroll
+            for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
+                dots[hl] += row_ror<8>(dots[hl]);
+            }
+#pragma unroll
+            for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
+                dots[hl] += row_ror<4>(dots[hl]);
+            }
+#pragma unroll
+            for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
+                dots[hl] += row_ror<2>(dots[hl]);
+            }
+#pragma unroll
+            for (int hl = 0; hl < kHeadsPerGroup; ++hl) {
+                dots[hl] += row_ror<1>(dots[hl]);
+            }
+            float mine = dots[0];
+#pragma unroll
+            for (int hl = 1; hl < kHeadsPerGroup; ++hl) {
+                mine = li == hl ? dots[hl] : mine;
+            }
+            const int tok = kFlatTokens * u + gi;
+            if (li < kHeadsPerGroup) {
+                s_sc[li][tok] = mine * a.qk_scale_log2;  // score of (token tok, head li)
+            }
+            float4* vrow = reinterpret_cast<float4*>(&s_vf[tok][8 * li]);
+            vrow[0] = make_float4(vf[0], vf[1], vf[2], vf[3]);
+            vrow[1] = make_float4(vf[4], vf[5], vf[6], vf[7]);
+        }
+        __syncthreads();
+        {
+            const int hl = threadIdx.x / (2 * kGroups);
+            const int gg = threadIdx.x % (2 * kGroups);
+            float M = kNegInf;
+#pragma unroll 8
+            for (int x = 0; x < 2 * kGroups; ++x) {
+                M = x < nvalid ? fmaxf(M, s_sc[hl][x]) : M;
+            }
+            s_wt[hl][gg] = gg < nvalid ? exp2_fixed(s_sc[hl][gg] - M) : 0.0f;
+            if (gg == 0) {
+                s_M[hl] = M;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const int hl = half * 4 + threadIdx.x / kDim;
+            const int dd = threadIdx.x % kDim;
+            float acc_f = 0.0f;
+            float lsum = 0.0f;
+#pragma unroll 8
+            for (int x = 0; x < nvalid; ++x) {
+                const float w = s_wt[hl][x];
                 acc_f = fmaf(w, s_vf[x][dd], acc_f);
                 lsum = lsum + w;
             }
@@ -666,7 +769,9 @@ __global__ __launch_bounds__(256) void gqa_merge_kernel(GqaArgs a) {
 }  // namespace
 
 // Split rule (measured on MI355X): flat path up to 32 x 32 tokens (585-1024
-// tokens: 13.4 -> 8.9 us against 128-token round splits); round path with
+// tokens: 13.4 -> 8.9 us against 128-token round splits) and up to 32 x 64
+// tokens with two tokens per group (1100-2048 tokens: 13.3-13.7 -> 12.2-12.7
+// us); round path with
 // 128-token splits up to 8192 tokens (more blocks at mid lengths: 8192 tokens
 // 17.7 -> 15.3 us against 256-token splits), 256-token splits
 // beyond (at 32768 tokens 256 splits of 128 cost more in the merge than they

@@ -41,10 +41,13 @@ struct AttnSplits {
     int64_t defer_max = 0;
 };
 
-// Tokens per split at kv_len L: flat path (kGqaFlatTokens) up to flat_max,
-// round path with kGqaMidTokens up to mid_max and `chunk` beyond.
+// Tokens per split at kv_len L: flat path (kGqaFlatTokens, one per group)
+// up to flat_max, flat path with two tokens per group up to 2 * flat_max
+// (the same number of splits at most), round path with kGqaMidTokens up to
+// mid_max and `chunk` beyond.
 __host__ __device__ inline int64_t gqa_split_tokens(int64_t L, int64_t flat_max, int64_t mid_max, int64_t chunk) {
-    return L <= flat_max ? kGqaFlatTokens : (L <= mid_max ? kGqaMidTokens : chunk);
+    return L <= flat_max ? kGqaFlatTokens
+                         : (L <= 2 * flat_max ? 2 * kGqaFlatTokens : (L <= mid_max ? kGqaMidTokens : chunk));
 }
 __host__ __device__ inline int64_t gqa_split_count(int64_t L, int64_t flat_max, int64_t mid_max, int64_t chunk) {
     const int64_t c = gqa_split_tokens(L, flat_max, mid_max, chunk);

@@ -383,7 +383,8 @@ KCO_API void kco_down11008(int act, const uint16_t* x, const uint8_t* w, const f
 #define GQA_ROUND (4 * GQA_GROUPS)
 
 /* Flat path: kv_len <= flat_max, GQA_GROUPS tokens per split (one per group),
- * at most GQA_FLAT_SPLITS splits. */
+ * at most GQA_FLAT_SPLITS splits; kv_len <= 2 * flat_max, two tokens per
+ * group (the same split count). */
 #define GQA_FLAT_SPLITS 32
 
 /* tokens per split on the round path for a cache of `tokens` rows */
@@ -434,16 +435,19 @@ static void gqa_scores(int act, const float qf[8][128], const uint16_t* krow, fl
 }
 
 /* q [16,128], caches [2, capacity, 128], kv_len L; flat path for
- * L <= flat_max, else the round path with GQA_ROUND-token splits for
- * L <= mid_max and `chunk`-token splits (a multiple of GQA_ROUND) beyond. */
+ * L <= flat_max (GQA_GROUPS tokens per split) and L <= 2 * flat_max
+ * (2 * GQA_GROUPS tokens per split), else the round path with
+ * GQA_ROUND-token splits for L <= mid_max and `chunk`-token splits (a
+ * multiple of GQA_ROUND) beyond. */
 KCO_API void kco_gqa(int act, const uint16_t* q, const uint16_t* kc, const uint16_t* vc, int64_t capacity,
                      int64_t L, int64_t chunk, int64_t flat_max, int64_t mid_max, float qk_scale_log2,
                      uint16_t* out) {
     if (L > capacity) L = capacity;
     if (L < 1) return;
-    const int flat = L <= flat_max;
+    const int flat = L <= 2 * flat_max;
+    const int64_t tps = L <= flat_max ? GQA_GROUPS : 2 * GQA_GROUPS; /* flat tokens per split */
     const int64_t C = L <= mid_max ? GQA_ROUND : chunk;
-    const int64_t nsplit = flat ? (L + GQA_GROUPS - 1) / GQA_GROUPS : (L + C - 1) / C;
+    const int64_t nsplit = flat ? (L + tps - 1) / tps : (L + C - 1) / C;
     float* part = (float*)malloc(sizeof(float) * 16 * (size_t)nsplit * 130);
 #pragma omp parallel for collapse(2) schedule(static)
     for (int g = 0; g < 2; ++g) {
@@ -452,18 +456,19 @@ KCO_API void kco_gqa(int act, const uint16_t* q, const uint16_t* kc, const uint1
             for (int hl = 0; hl < 8; ++hl)
                 for (int d = 0; d < 128; ++d) qf[hl][d] = act_load(act, q[(8 * g + hl) * 128 + d]);
             if (flat) {
-                /* one token per group; per head: M = max, w_t = exp2(s_t - M),
-                 * l = sum of w_t and acc = sum of w_t v_t, both in token order */
-                const int64_t f0 = s * GQA_GROUPS;
-                const int nvalid = (int)(f0 + GQA_GROUPS < L ? GQA_GROUPS : L - f0);
-                float sc[GQA_GROUPS][8];
+                /* one or two tokens per group; per head: M = max,
+                 * w_t = exp2(s_t - M), l = sum of w_t and acc = sum of w_t v_t,
+                 * both in token order */
+                const int64_t f0 = s * tps;
+                const int nvalid = (int)(f0 + tps < L ? tps : L - f0);
+                float sc[2 * GQA_GROUPS][8];
                 for (int t = 0; t < nvalid; ++t)
                     gqa_scores(act, (const float(*)[128])qf, kc + ((int64_t)g * capacity + f0 + t) * 128,
                                qk_scale_log2, sc[t]);
                 for (int hl = 0; hl < 8; ++hl) {
                     float M = -INFINITY;
                     for (int t = 0; t < nvalid; ++t) M = fmaxf(M, sc[t][hl]);
-                    float w[GQA_GROUPS];
+                    float w[2 * GQA_GROUPS];
                     float lsum = 0.0f;
                     for (int t = 0; t < nvalid; ++t) {
                         w[t] = exp2_fixed(sc[t][hl] - M);

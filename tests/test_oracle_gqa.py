@@ -104,16 +104,17 @@ def test_split_plan_covers_every_regime():
     assert splits == 8 and chunk * 8 >= 32768 and mid_max == 1024
 
 
-@pytest.mark.parametrize("kv_len", [31, 32, 33, 200, 511, 512, 513, 600])
+@pytest.mark.parametrize("kv_len", [31, 32, 33, 200, 1023, 1024, 1025, 1087, 2047, 2048, 2049, 2100])
 def test_flat_path_boundaries_match_fp64(kv_len):
     """Split edges of the flat path (a full split, a one-token split, the
-    16-split maximum) and the first lengths past it (round path, 128-token
+    32-split maximum), of its two-token-per-group form (64-token splits up to
+    2048 tokens) and the first lengths past it (round path, 128-token
     splits)."""
 
     rng = np.random.default_rng([7, kv_len])
     q = O.f32_to_bf16(rng.standard_normal(2048).astype(F))
-    k = O.f32_to_bf16(rng.standard_normal((2, 600, 128)).astype(F))
-    v = O.f32_to_bf16(rng.standard_normal((2, 600, 128)).astype(F))
+    k = O.f32_to_bf16(rng.standard_normal((2, 2100, 128)).astype(F))
+    v = O.f32_to_bf16(rng.standard_normal((2, 2100, 128)).astype(F))
     got = O.bf16_to_f32(O.gqa(q, k, v, kv_len))
     want = gqa_f64(O.bf16_to_f32(q), O.bf16_to_f32(k), O.bf16_to_f32(v), kv_len, SCALE)
     assert np.all(np.abs(got - want) <= 2.0 ** -8 * np.abs(want) + 2e-4)

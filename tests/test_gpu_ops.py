@@ -260,8 +260,9 @@ def test_gqa_workspace_v3(torch_gpu, native, stream):
     capacity = 512
     scale = synthetic.default_scale()
     ws = empty(torch, 16 * 8 * 130, "f32")
-    # reference tests/qwen2_gqa_workspace_smoke.cu:29-49, plus the edge of the
-    # flat path under this 8-split workspace (256 flat, 257 round)
+    # reference tests/qwen2_gqa_workspace_smoke.cu:29-49, plus the edges of the
+    # flat path under this 8-split workspace (256: one token per group; 257 and
+    # 512: two tokens per group)
     for kv_len in (1, 7, 64, 128, 256, 257, 512):
         q, k, v = synthetic.gqa_inputs(SEED + kv_len, kv_len, capacity)
         q16 = O.f32_to_f16(O.bf16_to_f32(q))

@@ -669,8 +669,8 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a) {
     // and sums of its head and its element of every split's accumulator),
     // then forms the weights exp2(m_s - M) itself and sums in split order.
     // Up to 16 splits use 16-wide register arrays, more the 32-wide ones
-    // (same operations in the same order; the narrow form keeps the common
-    // short merges as cheap as before).
+    // (same operations in the same order; short merges do not pay for the
+    // wide form's loads and instructions).
     if (nsplit <= kInKernelSplits / 2) {
         ticket_merge<T, kInKernelSplits / 2>(a, part, g, static_cast<int>(nsplit));
     } else {

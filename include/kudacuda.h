@@ -234,6 +234,23 @@ KUDACUDA_API int kudacuda_qwen2_gqa_decode_graph_bf16(void* handle, uint64_t que
                                                       int64_t kv_heads, int64_t head_dim, float scale,
                                                       uint64_t kv_len_device, uint64_t stream);
 
+/* NEW — no counterpart in the reference: the allocation-free twin of
+ * kudacuda_qwen2_gqa_decode_graph_bf16 (same arguments, same kernels, same
+ * results) for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Its
+ * split partials and ticket counters live in a fixed static device array of
+ * the library (~4.3 MB per GPU, held until the process ends) instead of the
+ * handle's scratch; the call itself allocates nothing.  kv_capacity 1..32768
+ * (larger is rejected with status 1).  Every call on one GPU shares that
+ * array, so calls that overlap on one GPU (two streams, two handles) race;
+ * serialise them. */
+KUDACUDA_API int kudacuda_qwen2_gqa_decode_graph_bf16_noalloc(void* handle, uint64_t query, uint64_t key_cache,
+                                                              uint64_t value_cache, uint64_t output,
+                                                              int64_t batch_size, int64_t query_len,
+                                                              int64_t kv_capacity, int64_t query_heads,
+                                                              int64_t kv_heads, int64_t head_dim, float scale,
+                                                              uint64_t kv_len_device, uint64_t stream);
+
 /* NEW — split-KV chunk (tokens per split) and fp32 workspace size used for a
  * given cache length; the decoder sizes its attention workspace with it. */
 KUDACUDA_API int64_t kudacuda_gqa_split_chunk(int64_t kv_tokens);

@@ -58,6 +58,7 @@ SIGNATURES: dict[str, tuple[list[Any], Any]] = {
     "kudacuda_qwen2_gqa_decode_vectorized": ([_vp] + [_u64] * 4 + [_i64] * 6 + [_f, _u64], _i),
     "kudacuda_qwen2_gqa_decode_bf16": ([_vp] + [_u64] * 4 + [_i64] * 6 + [_f, _u64], _i),
     "kudacuda_qwen2_gqa_decode_graph_bf16": ([_vp] + [_u64] * 4 + [_i64] * 6 + [_f, _u64, _u64], _i),
+    "kudacuda_qwen2_gqa_decode_graph_bf16_noalloc": ([_vp] + [_u64] * 4 + [_i64] * 6 + [_f, _u64, _u64], _i),
     "kudacuda_gqa_split_chunk": ([_i64], _i64),
     "kudacuda_gqa_workspace_floats": ([_i64], _i64),
     "kudacuda_lm_head_argmax_bf16": ([_vp] + [_u64] * 5 + [_i64, _i64, _f, _u64], _i),

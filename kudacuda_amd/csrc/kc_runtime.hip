@@ -12,6 +12,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -25,6 +26,57 @@ namespace {
 
 constexpr int64_t kMaxStandaloneKv = 65536;
 constexpr int64_t kMaxModelKv = 32768;
+
+// ------------------------------------------------ allocation-free scratch
+// Device scratch of kudacuda_qwen2_gqa_decode_graph_bf16_noalloc: the split
+// partials (16 heads x splits x 130 fp32) and the two ticket counters of the
+// split-KV attention, in one file-scope device array per GPU (the code object
+// holds one copy per device; it lives until the process ends).  Layout:
+// bytes [0, 256) counters (uint32 [2], zero between calls), then the partials.
+// Host code never passes `scratch` itself to a kernel: its name is a host-side
+// stand-in, so every use goes through the device address that
+// hipGetSymbolAddress returned on that device (static_scratch_on()).
+constexpr int64_t kNoAllocMaxKv = 32768;
+constexpr int64_t kNoAllocMaxSplits = 512;
+constexpr int64_t kNoAllocCounterBytes = 256;
+constexpr int64_t kNoAllocPartialFloats = 16 * kNoAllocMaxSplits * kGqaPartialStride;
+constexpr int64_t kNoAllocScratchBytes = kNoAllocCounterBytes + kNoAllocPartialFloats * 4;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Resolve this device's copy of `scratch` (call with `device` current) and
+// zero its counters once; later calls return the recorded address.  Runs in
+// kudacuda_create, never under stream capture.
+hipError_t setup_static_scratch(int device, void** out) {
+    *out = nullptr;
+    if (device < 0 || device >= kMaxDevices) {
+        return hipErrorInvalidDevice;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[device] == nullptr) {
+        void* p = nullptr;
+        hipError_t status = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (status != hipSuccess) {
+            return status;
+        }
+        if (p == nullptr) {
+            return hipErrorInvalidSymbol;
+        }
+        status = hipMemset(p, 0, static_cast<size_t>(kNoAllocCounterBytes));
+        if (status == hipSuccess) {
+            status = hipDeviceSynchronize();
+        }
+        if (status != hipSuccess) {
+            return status;
+        }
+        g_scratch_ptr[device] = p;
+    }
+    *out = g_scratch_ptr[device];
+    return hipSuccess;
+}
 
 struct Handle {
     explicit Handle(int id) : device_id(id) {}
@@ -58,6 +110,8 @@ struct Handle {
     float* lm_best = nullptr;
     uint32_t* counters = nullptr;  // [0..1] attention, [2] lm_head
     int32_t* argmax_slot = nullptr;
+    // this device's copy of the file-scope `scratch` array (device address)
+    unsigned char* static_scratch = nullptr;
 };
 
 Handle* as_handle(void* raw) { return reinterpret_cast<Handle*>(raw); }
@@ -253,8 +307,11 @@ int gqa_direct(void* raw, const char* symbol, Act act, uint64_t q, uint64_t k, u
     return finish(h, symbol, launch_gqa_decode(act, a, as_stream(stream)));
 }
 
+// no_alloc: split partials and counters come from this device's copy of the
+// file-scope `scratch` array instead of the handle's allocation
 int gqa_graph(void* raw, const char* symbol, Act act, uint64_t q, uint64_t k, uint64_t v, uint64_t out,
-              const GqaShape& s, int64_t kv_capacity, uint64_t kv_len_device, uint64_t stream) {
+              const GqaShape& s, int64_t kv_capacity, uint64_t kv_len_device, uint64_t stream,
+              bool no_alloc = false) {
     Handle* h = as_handle(raw);
     const std::string name = std::string("kudacuda_") + symbol;
     if (!ready(h, name.c_str())) {
@@ -264,7 +321,7 @@ int gqa_graph(void* raw, const char* symbol, Act act, uint64_t q, uint64_t k, ui
         h->set_error(std::string(symbol) + " requires non-null device pointers");
         return 1;
     }
-    if (!gqa_shape_ok(h, symbol, s, "kv_capacity", kv_capacity, kMaxStandaloneKv)) {
+    if (!gqa_shape_ok(h, symbol, s, "kv_capacity", kv_capacity, no_alloc ? kNoAllocMaxKv : kMaxStandaloneKv)) {
         return 1;
     }
     GqaArgs a;
@@ -272,10 +329,24 @@ int gqa_graph(void* raw, const char* symbol, Act act, uint64_t q, uint64_t k, ui
     a.k = ptr<const uint16_t>(k);
     a.v = ptr<const uint16_t>(v);
     a.out = ptr<uint16_t>(out);
-    a.partials = h->gqa_partials;
-    a.counters = h->counters;
     a.kv_len_device = ptr<const int32_t>(kv_len_device);
     set_gqa_plan(a, kv_capacity, 0);
+    if (no_alloc) {
+        if (h->static_scratch == nullptr) {
+            h->set_error(std::string(symbol) + ": the static device scratch of this device is not set up");
+            return 1;
+        }
+        if (16 * a.max_splits * kGqaPartialStride > kNoAllocPartialFloats) {
+            h->set_error(std::string(symbol) + ": kv_capacity " + std::to_string(kv_capacity) +
+                         " needs more split partials than the static scratch holds");
+            return 1;
+        }
+        a.counters = reinterpret_cast<uint32_t*>(h->static_scratch);
+        a.partials = reinterpret_cast<float*>(h->static_scratch + kNoAllocCounterBytes);
+    } else {
+        a.partials = h->gqa_partials;
+        a.counters = h->counters;
+    }
     a.qk_scale_log2 = s.scale * kLog2e;
     return finish(h, symbol, launch_gqa_decode(act, a, as_stream(stream)));
 }
@@ -655,6 +726,13 @@ void* kudacuda_create(int device_id) {
         h->set_hip_error("hipMemset(handle counters)", status);
         return h;
     }
+    void* static_scratch = nullptr;
+    status = kc::setup_static_scratch(device_id, &static_scratch);
+    if (status != hipSuccess) {
+        h->set_hip_error("hipGetSymbolAddress(scratch)", status);
+        return h;
+    }
+    h->static_scratch = static_cast<unsigned char*>(static_scratch);
     h->device_ready = true;
     return h;
 }
@@ -1119,6 +1197,16 @@ int kudacuda_qwen2_gqa_decode_graph_bf16(void* raw, uint64_t query, uint64_t key
     return kc::gqa_graph(raw, "qwen2_gqa_decode_graph_bf16", Act::kBf16, query, key_cache, value_cache, output,
                          {batch_size, query_len, query_heads, kv_heads, head_dim, scale}, kv_capacity, kv_len_device,
                          stream);
+}
+
+int kudacuda_qwen2_gqa_decode_graph_bf16_noalloc(void* raw, uint64_t query, uint64_t key_cache,
+                                                 uint64_t value_cache, uint64_t output, int64_t batch_size,
+                                                 int64_t query_len, int64_t kv_capacity, int64_t query_heads,
+                                                 int64_t kv_heads, int64_t head_dim, float scale,
+                                                 uint64_t kv_len_device, uint64_t stream) {
+    return kc::gqa_graph(raw, "qwen2_gqa_decode_graph_bf16_noalloc", Act::kBf16, query, key_cache, value_cache,
+                         output, {batch_size, query_len, query_heads, kv_heads, head_dim, scale}, kv_capacity,
+                         kv_len_device, stream, true);
 }
 
 int kudacuda_qwen2_gqa_decode_group_tiled(void* raw, uint64_t query, uint64_t key_cache, uint64_t value_cache,

@@ -249,7 +249,7 @@ def main(argv: list[str] | None = None) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "bf16",
         "data": "synthetic",
         "config": {
             "workload": "qwen2.5-3b-shape NF4 batch-1 greedy decode, hipGraph per token",

@@ -189,6 +189,14 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_partial_kernel(GqaArgs a) {
     const int64_t L = read_kv_len(a);
     const int64_t nsplit = split_count(a, L);
     if (s >= nsplit) {
+        if (nsplit == 0 && s == 0) {
+            // empty cache (device kv_len <= 0): zero output, as the reference
+            // workspace kernel writes (qwen2_gqa_workspace.cuh:118)
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                a.out[(g * kHeadsPerGroup) * kDim + threadIdx.x + k * kGqaThreads] = 0;
+            }
+        }
         return;
     }
     const int64_t C = gqa_split_tokens(L, a.flat_max, a.mid_max, a.chunk);

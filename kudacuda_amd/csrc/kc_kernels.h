@@ -206,7 +206,7 @@ struct GqaArgs {
     int64_t flat_max = 0;          // kv_len <= flat_max takes the flat path (kGqaFlatTokens per split)
     int64_t mid_max = 0;           // flat_max < kv_len <= mid_max: round path, kGqaMidTokens per split
     int64_t defer_max = 0;         // <= kGqaMaxDefer: partials left for the consumer up to this many splits
-    // 1..16: splits the partial kernel merges itself (merge kernel beyond).
+    // 1..32: splits the partial kernel merges itself (merge kernel beyond).
     // Measured: the merge kernel matches the ticket at 2-4 splits and beats
     // it from ~9 (512 tokens: 11.1 -> 8.5 us), so standalone calls use 4.
     int64_t ticket_max = 4;

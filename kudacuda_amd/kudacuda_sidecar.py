@@ -55,6 +55,14 @@ class NativeCudaError(RuntimeError):
     """The native library rejected a request or a launch failed."""
 
 
+class CacheCommittedError(NativeCudaError):
+    """Attention failed after this token was already written to the KV cache.
+
+    The Transformers guards re-raise it instead of running the framework's
+    forward: that forward would update the cache a second time and every
+    later step would attend to a duplicated key/value row."""
+
+
 def _normalize_cuda_handle(value: int) -> int:
     """PyTorch reports stream handles as signed integers; the ABI takes uint64."""
 
@@ -212,6 +220,66 @@ def _qwen2_attention_dimensions(module: Any) -> tuple[int, int, int]:
         hidden = int(getattr(config, "hidden_size", 0))
         head_dim = hidden // int(heads) if heads else 0
     return int(heads), int(kv_heads), int(head_dim)
+
+
+# positional parameters of Qwen2Attention.forward after hidden_states
+_ATTENTION_POSITIONAL = ("position_embeddings", "attention_mask", "past_key_values", "cache_position")
+
+
+@dataclass
+class _AttentionCall:
+    """One Qwen2 attention call as the dispatcher sees it: its arguments bound
+    by name, the head layout, and whether the KV cache has taken the token."""
+
+    module: Any
+    hidden_states: Any
+    position_embeddings: Any
+    mask: Any
+    cache: Any
+    cache_position: Any
+    output_attentions: bool
+    heads: int
+    kv_heads: int
+    head_dim: int
+    committed: bool = False
+
+    @classmethod
+    def bind(cls, module: Any, hidden_states: Any, args: tuple[Any, ...], kwargs: Mapping[str, Any]) -> "_AttentionCall":
+        named = dict(zip(_ATTENTION_POSITIONAL, args))
+        for name in _ATTENTION_POSITIONAL:
+            if kwargs.get(name) is not None:
+                named[name] = kwargs[name]
+        if named.get("past_key_values") is None and kwargs.get("past_key_value") is not None:
+            named["past_key_values"] = kwargs["past_key_value"]  # older Transformers spelling
+        heads, kv_heads, head_dim = _qwen2_attention_dimensions(module)
+        return cls(module, hidden_states, named.get("position_embeddings"), named.get("attention_mask"),
+                   named.get("past_key_values"), named.get("cache_position"),
+                   bool(kwargs.get("output_attentions", False)), heads, kv_heads, head_dim)
+
+    @property
+    def lead(self) -> tuple[int, ...]:
+        return tuple(self.hidden_states.shape[:-1])
+
+    def admission_refusal(self, graph_mode: bool) -> Optional[str]:
+        """Why the native path cannot take this call, decided before anything
+        is computed or written; ``None`` admits it."""
+
+        shape = _shape(self.hidden_states)
+        if len(shape) != 3 or shape[:2] != (1, 1):
+            return f"shape:{shape}"
+        if self.output_attentions:
+            return "output_attentions"
+        for label, value, want in (("query_heads", self.heads, 16), ("kv_heads", self.kv_heads, 2),
+                                   ("head_dim", self.head_dim, 128)):
+            if value != want:
+                return f"{label}:{value}"
+        if self.position_embeddings is None:
+            return "missing_position_embeddings"
+        if graph_mode and getattr(self.module, "sliding_window", None) is not None:
+            return "graph_sliding_window_unsupported"
+        if not graph_mode and self.mask is not None and _rank(self.mask) != 4:
+            return f"attention_mask_shape:{_shape(self.mask)}"
+        return None
 
 
 # GQA tactic variant (name suffix) -> (fp16 symbol, bf16 symbol)
@@ -637,122 +705,123 @@ class KudaCudaBridge:
         """Qwen2 decode attention through the native kernel, or ``None`` so the
         caller runs the framework's own forward.
 
-        Same division of work as reference python/kudacuda_sidecar.py:767-958:
-        Transformers keeps projections (unless a fused QKV hook pre-computed
-        them), rotary embedding, the cache update and o_proj; the native
-        kernel owns attention over the materialised contiguous cache.  The
-        reason of the last decision is left in ``last_qwen2_dispatch_reason``.
+        The division of work is the reference's (python/kudacuda_sidecar.py:
+        767-958): Transformers keeps the projections (unless the fused QKV
+        hook pre-computed them), rotary embedding, the cache update and
+        o_proj, and the native kernel runs attention over the materialised
+        contiguous cache.  The call runs in two phases:
+
+        * admission, free of side effects: token shape, head layout, rotary
+          inputs, mask rank and the graph-mode limits.  A refusal returns
+          ``None`` and the framework forward runs as if no hook existed;
+        * execution: projections, rotary, then the cache update.  From that
+          update on the cache holds this token, so the call always returns
+          the layer's attention output -- from the native kernel when the
+          cache and mask allow it, otherwise from the framework's eager
+          softmax on the same tensors (reason prefixed
+          ``framework_fallback:``).  When even that fails it raises
+          ``CacheCommittedError``, which the guards pass on instead of
+          re-running the forward (that would append the token twice).
+
+        The reason of the last decision is left in ``last_qwen2_dispatch_reason``.
         """
 
         import torch
 
         self.last_qwen2_dispatch_reason = "started"
-
-        def fallback(reason: str) -> None:
-            self.last_qwen2_dispatch_reason = reason
+        call = _AttentionCall.bind(module, hidden_states, args, kwargs)
+        graph_mode = (("graph_v1" in tactic_name or "workspace_v3" in tactic_name)
+                      and self._graph_kv_len_device is not None and self._graph_kv_capacity is not None)
+        refusal = call.admission_refusal(graph_mode)
+        if refusal is not None:
+            self.last_qwen2_dispatch_reason = refusal
             return None
 
-        shape = _shape(hidden_states)
-        if len(shape) != 3 or shape[:2] != (1, 1):
-            return fallback(f"shape:{shape}")
-        if bool(kwargs.get("output_attentions", False)):
-            return fallback("output_attentions")
-        heads, kv_heads, head_dim = _qwen2_attention_dimensions(module)
-        for label, value, want in (("query_heads", heads, 16), ("kv_heads", kv_heads, 2),
-                                   ("head_dim", head_dim, 128)):
-            if value != want:
-                return fallback(f"{label}:{value}")
-
-        rest = list(args)
-        position_embeddings = kwargs.get("position_embeddings")
-        attention_mask = kwargs.get("attention_mask")
-        past_key_values = kwargs.get("past_key_values")
-        if position_embeddings is None and rest:
-            position_embeddings = rest.pop(0)
-        if attention_mask is None and rest:
-            attention_mask = rest.pop(0)
-        if past_key_values is None and rest:
-            past_key_values = rest.pop(0)
-        if position_embeddings is None:
-            return fallback("missing_position_embeddings")
-
-        state: dict[str, Any] = {"cache_updated": False, "graph_mode": False}
         try:
             from transformers.models.qwen2.modeling_qwen2 import apply_rotary_pos_emb
 
-            lead = tuple(hidden_states.shape[:-1])
-            query, key, value = self._qwen2_projections(module, hidden_states, lead)
-            cos, sin = position_embeddings
+            query, key, value = self._qwen2_projections(module, hidden_states, call.lead)
+            cos, sin = call.position_embeddings
             query, key = apply_rotary_pos_emb(query, key, cos, sin)
-            if past_key_values is not None:
-                key, value = self._qwen2_cache_update(module, past_key_values, key, value, cos, sin,
-                                                      kwargs.get("cache_position"))
-                state["cache_updated"] = True
-            state.update(query=query, key=key, value=value)
-            if key.dim() != 4 or value.shape != key.shape:
-                return fallback(f"cache_shape:{tuple(key.shape)}:{tuple(value.shape)}")
-            graph_mode = (("graph_v1" in tactic_name or "workspace_v3" in tactic_name)
-                          and self._graph_kv_len_device is not None and self._graph_kv_capacity is not None)
-            state["graph_mode"] = graph_mode
-            kv_len = int(key.shape[-2])
-            if graph_mode:
-                if kv_len != self._graph_kv_capacity:
-                    return fallback(f"graph_cache_capacity:{kv_len}:{self._graph_kv_capacity}")
-                if getattr(module, "sliding_window", None) is not None:
-                    return fallback("graph_sliding_window_unsupported")
-
-            def eager(reason: str) -> Any:
-                self.last_qwen2_dispatch_reason = reason
-                return self._qwen2_eager_attention(torch, module, query, key, value, attention_mask, lead,
-                                                   heads // kv_heads, head_dim)
-
-            if attention_mask is not None and not graph_mode:
-                if attention_mask.dim() != 4 or int(attention_mask.shape[-1]) != kv_len:
-                    return fallback(f"attention_mask_shape:{tuple(attention_mask.shape)}:kv={kv_len}")
-                if not bool(torch.all(attention_mask == 0)):
-                    return eager("framework_fallback:attention_mask_values")
-            if graph_mode:
-                query, key, value = query.contiguous(), key.contiguous(), value.contiguous()
-            elif not (query.is_contiguous() and key.is_contiguous()):
-                return eager(f"non_contiguous:q={query.stride()}:k={key.stride()}")
-
-            output = torch.empty_like(query)
-            stream_ptr = int(torch.cuda.current_stream(hidden_states.device).cuda_stream)
+        except Exception as error:  # nothing is written yet: the framework can redo it all
+            self.last_qwen2_dispatch_reason = f"exception:{type(error).__name__}:{error}"
+            return None
+        if call.cache is not None:
+            call.committed = True  # a failing update may already have appended
             try:
-                if "workspace_v3" in tactic_name:
-                    if self._graph_workspace is None:
-                        raise NativeCudaError("workspace GQA tactic requires a configured workspace")
-                    self.dispatch_qwen2_gqa_decode_workspace(
-                        query, key, value, output, kv_capacity=int(self._graph_kv_capacity or 0),
-                        kv_len_device=self._graph_kv_len_device, workspace=self._graph_workspace,
-                        stream_ptr=stream_ptr, tactic_name=tactic_name)
-                elif graph_mode:
-                    self.dispatch_qwen2_gqa_decode_graph(
-                        query, key, value, output, kv_capacity=int(self._graph_kv_capacity or 0),
-                        kv_len_device=self._graph_kv_len_device, stream_ptr=stream_ptr, tactic_name=tactic_name)
-                else:
-                    self.dispatch_qwen2_gqa_decode(query, key, value, output, kv_len=kv_len, stream_ptr=stream_ptr,
-                                                   tactic_name=tactic_name)
+                key, value = self._qwen2_cache_update(module, call.cache, key, value, cos, sin, call.cache_position)
             except Exception as error:
+                raise CacheCommittedError(f"KV cache update failed: {type(error).__name__}: {error}") from error
+
+        route = self._attention_route(torch, call, query, key, value, graph_mode)
+        if route == "native":
+            try:
                 if graph_mode:
+                    query, key, value = query.contiguous(), key.contiguous(), value.contiguous()
+                context = self._attention_native(torch, hidden_states, query, key, value, tactic_name, graph_mode)
+                self.last_qwen2_dispatch_reason = "native"
+                return module.o_proj(context.transpose(1, 2).reshape(*call.lead, -1).contiguous()), None
+            except Exception as error:
+                if graph_mode:  # a capture must not silently record framework attention
+                    if call.committed:
+                        raise CacheCommittedError(f"native graph attention failed: {error}") from error
                     raise
-                return eager(f"framework_fallback:native_exception:{type(error).__name__}:{error}")
-            attn = output.transpose(1, 2).reshape(*lead, -1).contiguous()
-            self.last_qwen2_dispatch_reason = "native"
-            return module.o_proj(attn), None
+                route = f"framework_fallback:native_exception:{type(error).__name__}:{error}"
+        self.last_qwen2_dispatch_reason = route
+        try:
+            return self._qwen2_eager_attention(torch, module, query, key, value, call.mask, call.lead,
+                                               call.heads // call.kv_heads, call.head_dim)
         except Exception as error:
-            if state["graph_mode"]:
-                raise
-            if state["cache_updated"] and "query" in state:
-                # the cache already holds this token: finish in the framework
-                try:
-                    self.last_qwen2_dispatch_reason = f"framework_fallback:exception:{type(error).__name__}:{error}"
-                    return self._qwen2_eager_attention(torch, module, state["query"], state["key"], state["value"],
-                                                       attention_mask, tuple(hidden_states.shape[:-1]),
-                                                       heads // kv_heads, head_dim)
-                except Exception:
-                    pass
-            return fallback(f"exception:{type(error).__name__}:{error}")
+            if not call.committed:
+                self.last_qwen2_dispatch_reason = f"exception:{type(error).__name__}:{error}"
+                return None
+            raise CacheCommittedError(f"attention after the cache update failed ({route}): {error}") from error
+
+    def _attention_route(self, torch: Any, call: "_AttentionCall", query: Any, key: Any, value: Any,
+                         graph_mode: bool) -> str:
+        """``"native"`` when the native kernel can take the materialised
+        tensors, else the reason the framework's eager softmax runs instead."""
+
+        if key.dim() != 4 or tuple(value.shape) != tuple(key.shape):
+            return f"framework_fallback:cache_shape:{tuple(key.shape)}:{tuple(value.shape)}"
+        kv_len = int(key.shape[-2])
+        if graph_mode:
+            if kv_len != self._graph_kv_capacity:
+                return f"framework_fallback:graph_cache_capacity:{kv_len}:{self._graph_kv_capacity}"
+            return "native"
+        mask = call.mask
+        if mask is not None:
+            if int(mask.shape[-1]) != kv_len:
+                raise CacheCommittedError(f"attention mask covers {int(mask.shape[-1])} keys but the cache holds "
+                                          f"{kv_len}")
+            if not bool(torch.all(mask == 0)):
+                return "framework_fallback:attention_mask_values"
+        if not (query.is_contiguous() and key.is_contiguous()):
+            return f"framework_fallback:non_contiguous:q={query.stride()}:k={key.stride()}"
+        return "native"
+
+    def _attention_native(self, torch: Any, hidden_states: Any, query: Any, key: Any, value: Any, tactic_name: str,
+                          graph_mode: bool) -> Any:
+        """Launch the tactic's GQA entry point; returns [1, 16, 1, 128] like ``query``."""
+
+        output = torch.empty_like(query)
+        stream_ptr = int(torch.cuda.current_stream(hidden_states.device).cuda_stream)
+        capacity = int(self._graph_kv_capacity or 0)
+        if "workspace_v3" in tactic_name:
+            if self._graph_workspace is None:
+                raise NativeCudaError("workspace GQA tactic requires a configured workspace")
+            self.dispatch_qwen2_gqa_decode_workspace(query, key, value, output, kv_capacity=capacity,
+                                                     kv_len_device=self._graph_kv_len_device,
+                                                     workspace=self._graph_workspace, stream_ptr=stream_ptr,
+                                                     tactic_name=tactic_name)
+        elif graph_mode:
+            self.dispatch_qwen2_gqa_decode_graph(query, key, value, output, kv_capacity=capacity,
+                                                 kv_len_device=self._graph_kv_len_device, stream_ptr=stream_ptr,
+                                                 tactic_name=tactic_name)
+        else:
+            self.dispatch_qwen2_gqa_decode(query, key, value, output, kv_len=int(key.shape[-2]),
+                                           stream_ptr=stream_ptr, tactic_name=tactic_name)
+        return output
 
     @staticmethod
     def _qwen2_projections(module: Any, hidden_states: Any, lead: tuple[int, ...]) -> tuple[Any, Any, Any]:
@@ -1150,6 +1219,8 @@ def patch_qwen2_attention(bridge: Any, *, attention_cls: Any = None,
                 result = dispatcher(self, hidden_states, *args, tactic_name=tactic_name, **kwargs)
                 if result is not None:
                     return result
+        except CacheCommittedError:
+            raise  # the cache already holds this token: running the forward again would duplicate it
         except Exception:
             pass
         return original(self, hidden_states, *args, **kwargs)
@@ -1278,6 +1349,8 @@ def patch_qwen2_swiglu(model: Any, bridge: Any, *, tactic_name: str = DEFAULT_SW
                          stream_ptr=_current_stream(torch_module, flat.device), tactic_name=tactic_name)
                 bridge.last_swiglu_dispatch_reason = "native"
                 return residual + layer.mlp.down_proj(state["output"].reshape(1, 1, _INTERMEDIATE))
+            except CacheCommittedError:
+                raise
             except Exception as error:
                 bridge.last_swiglu_dispatch_reason = f"fallback:{type(error).__name__}:{error}"
                 if residual is not None:
@@ -1363,13 +1436,17 @@ def patch_qwen2_fused_qkv(model: Any, bridge: Any, *, tactic_name: str = DEFAULT
                 bridge.last_qwen2_fused_qkv_dispatch_reason = "native"
                 attention._kudacuda_prefused_qkv = (state["query"], state["key"], state["value"])
                 out = attention(hidden_states, *args, **kwargs)
-                residual = hidden_states + (out[0] if isinstance(out, tuple) else out)
-                return residual + layer.mlp(layer.post_attention_layernorm(residual))
+            except CacheCommittedError:
+                raise
             except Exception as error:
                 bridge.last_qwen2_fused_qkv_dispatch_reason = f"fallback:{type(error).__name__}:{error}"
                 return original(hidden_states, *args, **kwargs)
             finally:
                 _restore_attr(attention, "_kudacuda_prefused_qkv", previous)
+            # the attention (and its cache update) has run: finish the layer in
+            # the framework, never by re-running the whole forward
+            residual = hidden_states + (out[0] if isinstance(out, tuple) else out)
+            return residual + layer.mlp(layer.post_attention_layernorm(residual))
 
         return fused_forward
 

@@ -443,7 +443,12 @@ KCO_API void kco_gqa(int act, const uint16_t* q, const uint16_t* kc, const uint1
                      int64_t L, int64_t chunk, int64_t flat_max, int64_t mid_max, float qk_scale_log2,
                      uint16_t* out) {
     if (L > capacity) L = capacity;
-    if (L < 1) return;
+    if (L < 1) {
+        /* empty cache: zero output (reference qwen2_gqa_workspace.cuh:118,
+         * total > 0 ? weighted / total : 0) */
+        memset(out, 0, sizeof(uint16_t) * 16 * 128);
+        return;
+    }
     const int flat = L <= 2 * flat_max;
     const int64_t tps = L <= flat_max ? GQA_GROUPS : 2 * GQA_GROUPS; /* flat tokens per split */
     const int64_t C = L <= mid_max ? GQA_ROUND : chunk;

@@ -57,28 +57,67 @@ class F64Decoder:
         a, b = h[:, :64], h[:, 64:]
         return np.concatenate([a * c - b * s, b * c + a * s], axis=1).reshape(-1)
 
-    def step(self, token: int, pos: int) -> np.ndarray:
-        hidden = bits(self.embed[token])
-        for d in self.layers:
-            xn = self._norm(hidden, d["input_norm"])
-            q = rb(self._rope(d["q"] @ xn + d["q_bias"], pos))
-            k = rb(self._rope(d["k"] @ xn + d["k_bias"], pos))
-            v = rb(d["v"] @ xn + d["v_bias"])
-            d["K"][pos] = k.reshape(2, 128)
-            d["V"][pos] = v.reshape(2, 128)
+    def qkv(self, li: int, hidden: np.ndarray, pos: int) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+        """bf16-rounded q (after RoPE), k (after RoPE) and v of layer ``li``."""
+
+        d = self.layers[li]
+        xn = self._norm(hidden, d["input_norm"])
+        q = rb(self._rope(d["q"] @ xn + d["q_bias"], pos))
+        k = rb(self._rope(d["k"] @ xn + d["k_bias"], pos))
+        v = rb(d["v"] @ xn + d["v_bias"])
+        return q, k, v
+
+    @staticmethod
+    def attention(q: np.ndarray, keys: np.ndarray, vals: np.ndarray) -> np.ndarray:
+        """bf16-rounded softmax attention of q [2048] over keys/vals [2, L, 128]."""
+
+        att = np.empty((16, 128))
+        for h in range(16):
+            sc = keys[h // 8] @ q.reshape(16, 128)[h] / np.sqrt(128.0)
+            p = np.exp(sc - sc.max())
+            att[h] = (p / p.sum()) @ vals[h // 8]
+        return rb(att.reshape(-1))
+
+    def swiglu(self, li: int, hidden: np.ndarray) -> np.ndarray:
+        d = self.layers[li]
+        xn = self._norm(hidden, d["post_norm"])
+        g = d["gate"] @ xn
+        u = d["up"] @ xn
+        return rb(g / (1.0 + np.exp(-g)) * u)
+
+    def o_proj(self, li: int, att: np.ndarray) -> np.ndarray:
+        return rb(self.layers[li]["o"] @ att)
+
+    def down(self, li: int, h_mlp: np.ndarray) -> np.ndarray:
+        return rb(self.layers[li]["down"] @ h_mlp)
+
+    def layer(self, li: int, hidden: np.ndarray, pos: int, past_keys: np.ndarray | None = None,
+              past_values: np.ndarray | None = None) -> dict[str, np.ndarray]:
+        """Layer ``li`` at position ``pos`` on the fp64 residual stream
+        ``hidden``; returns the bf16-rounded query (after RoPE), attention
+        output, MLP intermediate and layer output.  With ``past_keys`` /
+        ``past_values`` ([2, pos, 128], e.g. another implementation's cache)
+        those rows are attended to instead of this decoder's own history."""
+
+        d = self.layers[li]
+        q, k, v = self.qkv(li, hidden, pos)
+        d["K"][pos] = k.reshape(2, 128)
+        d["V"][pos] = v.reshape(2, 128)
+        if past_keys is None:
             keys = np.stack([d["K"][p] for p in range(pos + 1)], axis=1)    # [2, L, 128]
             vals = np.stack([d["V"][p] for p in range(pos + 1)], axis=1)
-            att = np.empty((16, 128))
-            for h in range(16):
-                sc = keys[h // 8] @ q.reshape(16, 128)[h] / np.sqrt(128.0)
-                p = np.exp(sc - sc.max())
-                att[h] = (p / p.sum()) @ vals[h // 8]
-            att = rb(att.reshape(-1))
-            hidden = rb(hidden + rb(d["o"] @ att))
-            xn = self._norm(hidden, d["post_norm"])
-            g = d["gate"] @ xn
-            u = d["up"] @ xn
-            h_mlp = rb(g / (1.0 + np.exp(-g)) * u)
-            hidden = rb(hidden + rb(d["down"] @ h_mlp))
+        else:
+            keys = np.concatenate([past_keys, k.reshape(2, 1, 128)], axis=1)
+            vals = np.concatenate([past_values, v.reshape(2, 1, 128)], axis=1)
+        att = self.attention(q, keys, vals)
+        hidden = rb(hidden + self.o_proj(li, att))
+        h_mlp = self.swiglu(li, hidden)
+        hidden = rb(hidden + self.down(li, h_mlp))
+        return {"query": q, "attn": att, "mlp": h_mlp, "hidden": hidden}
+
+    def step(self, token: int, pos: int) -> np.ndarray:
+        hidden = bits(self.embed[token])
+        for li in range(len(self.layers)):
+            hidden = self.layer(li, hidden, pos)["hidden"]
         xn = self._norm(hidden, self.final_norm)
         return rb(bits(self.embed) @ xn)

@@ -4,7 +4,9 @@ Fixture = the seeded synthetic Qwen2.5-3B-shaped NF4 model (
 36 layers, vocab 151936, 64 random prompt ids, 128 greedy tokens, KV bucket
 2048) decoded by the oracle (oracle/kc_oracle.c), plus a 2-layer / 4096-vocab
 variant small enough for the CPU test suite.  Stored: prompt, generated ids,
-the bf16 top-1 minus top-2 logit margin at each generated token, and SHA-256
+the bf16 top-1 minus top-2 logit margin at each generated token, SHA-256
+digests of the bf16 logits and of the final hidden state (the residual stream
+after the last layer) after every step that emits a token, and SHA-256
 digests of the oracle-quantised layer-0 weights.
 
 Usage: python tests/golden/make_decode_golden.py [--small-only]
@@ -37,7 +39,7 @@ def run(name: str, *, num_layers: int, vocab: int, kv_capacity: int, prompt_len:
     t1 = time.time()
     prompt = synthetic.prompt_ids(SEED, prompt_len, vocab)
     model.reset(prompt)
-    margins = []
+    margins, logit_digests, hidden_digests = [], [], []
     for _ in range(prompt_len + new_tokens - 1):
         step = int(model.control[0])
         model.step()
@@ -45,6 +47,8 @@ def run(name: str, *, num_layers: int, vocab: int, kv_capacity: int, prompt_len:
             logits = O.bf16_to_f32(model.logits)
             top2 = np.sort(logits)[-2:]
             margins.append(float(top2[1] - top2[0]))
+            logit_digests.append(hashlib.sha256(model.logits.tobytes()).hexdigest())
+            hidden_digests.append(hashlib.sha256(model.hidden.tobytes()).hexdigest())
     tokens = model.tokens[prompt_len: prompt_len + new_tokens].astype(int).tolist()
     digests = {
         f"layer0_{n}": hashlib.sha256(model.layers[0][n].tobytes()).hexdigest()
@@ -53,7 +57,7 @@ def run(name: str, *, num_layers: int, vocab: int, kv_capacity: int, prompt_len:
     payload = {
         "seed": SEED, "num_layers": num_layers, "vocab": vocab, "kv_capacity": kv_capacity,
         "prompt": prompt.astype(int).tolist(), "tokens": tokens, "logit_margins": margins,
-        "weight_digests": digests, "generator": "tests/golden/make_decode_golden.py (oracle/kc_oracle.c)",
+        "logits_sha256": logit_digests, "hidden_sha256": hidden_digests, "weight_digests": digests, "generator": "tests/golden/make_decode_golden.py (oracle/kc_oracle.c)",
     }
     (OUT / f"{name}.json").write_text(json.dumps(payload, indent=1) + "\n", encoding="utf-8")
     print(f"{name}: build {t1 - t0:.1f}s decode {time.time() - t1:.1f}s tokens {tokens[:16]}... "

@@ -87,8 +87,8 @@ def test_generate_matches_oracle_tokens(small_pair):
 def test_long_context_decode_matches_oracle(torch_gpu, native, prompt_len, new, capacity):
     # Decode-step attention past the short-context regime: at 600+ cached
     # tokens the flat path runs 19-20 splits of 32 tokens, more than o_proj
-    # merges, so the attention kernel's in-kernel merge of up to 32 splits
-    # runs; past 1024 tokens the round path's 128-token splits take over.
+    # merges, so the attention kernel's in-kernel merge runs; at 1030-1038
+    # tokens the flat path takes two tokens per group (64-token splits).
     kw = dict(num_layers=2, vocab=4096, kv_capacity=capacity, token_capacity=capacity)
     gpu = Qwen2Nf4Decoder.synthetic(native, torch_gpu, seed=SEED, **kw)
     cpu = HostModel(SEED, **kw)
@@ -97,5 +97,45 @@ def test_long_context_decode_matches_oracle(torch_gpu, native, prompt_len, new, 
         assert np.array_equal(gpu.generate(prompt, new), cpu.generate(prompt, new))
         assert np.array_equal(host(gpu.logits), cpu.logits)
         assert np.array_equal(host(gpu.attn), cpu.attn)
+    finally:
+        gpu.close()
+
+
+@pytest.mark.parametrize("start,capacity", [(2100, 4096), (4200, 8192)])
+def test_decode_from_a_seeded_long_cache_matches_oracle(torch_gpu, native, start, capacity):
+    # The round path inside the decode step: both models get the same
+    # random cache rows 0..start-1 and decode from position start.  At 2100+
+    # tokens the 128-token splits number 17-18, merged by the attention
+    # kernel's ticket; at 4200 of an 8192-row cache they number 33+, past the
+    # ticket, so the step's separate merge kernel runs.
+    torch = torch_gpu
+    new = 6
+    kw = dict(num_layers=2, vocab=4096, kv_capacity=capacity, token_capacity=capacity)
+    gpu = Qwen2Nf4Decoder.synthetic(native, torch, seed=SEED, **kw)
+    cpu = HostModel(SEED, **kw)
+    try:
+        for li in range(2):
+            _, k, v = synthetic.gqa_inputs(SEED + 10 + li, start, capacity)
+            k = k.reshape(2, capacity, 128).copy()
+            v = v.reshape(2, capacity, 128).copy()
+            k[:, start:] = 0
+            v[:, start:] = 0
+            cpu.layers[li]["key_cache"][...] = k
+            cpu.layers[li]["value_cache"][...] = v
+            gpu.layers[li]["key_cache"].copy_(torch.from_numpy(k.view(np.int16)).view(torch.bfloat16))
+            gpu.layers[li]["value_cache"].copy_(torch.from_numpy(v.view(np.int16)).view(torch.bfloat16))
+        torch.cuda.synchronize()  # the copies ran on torch's current stream, the steps run on the model's
+        prompt = synthetic.prompt_ids(SEED + 4, start + 1, 4096)
+        gpu.reset(prompt, start_step=start)
+        cpu.reset(prompt, start_step=start)
+        for step in range(new):
+            gpu.step()
+            gpu.stream.synchronize()
+            cpu.step()
+            ctx = f"position {start + step}"
+            assert np.array_equal(host(gpu.attn), cpu.attn), ctx
+            assert np.array_equal(host(gpu.hidden), cpu.hidden), ctx
+            assert np.array_equal(host(gpu.logits), cpu.logits), ctx
+        assert np.array_equal(host(gpu.tokens)[: start + new + 1], cpu.tokens[: start + new + 1])
     finally:
         gpu.close()

@@ -277,6 +277,31 @@ def test_gqa_workspace_v3(torch_gpu, native, stream):
         assert np.array_equal(host(out), O.gqa(q16, k16, v16, kv_len, split_limit=8, dtype="f16"))
 
 
+@pytest.mark.parametrize("symbol", ["kudacuda_qwen2_gqa_decode_workspace_v3", "kudacuda_qwen2_gqa_decode_graph",
+                                    "kudacuda_qwen2_gqa_decode_graph_bf16"])
+@pytest.mark.parametrize("device_len", [0, -3])
+def test_gqa_empty_cache_writes_zeros(torch_gpu, native, stream, symbol, device_len):
+    # a device kv_len below 1 means an empty cache: the output is zero, as the
+    # reference workspace kernel writes (qwen2_gqa_workspace.cuh:118)
+    torch = torch_gpu
+    capacity = 512
+    q, k, v = synthetic.gqa_inputs(SEED, 1, capacity)
+    d_q, d_k, d_v = dev(torch, q), dev(torch, k), dev(torch, v)
+    d_len = dev(torch, np.array([device_len], dtype=np.int32))
+    out = dev(torch, np.full(2048, 0x3C00, dtype=np.uint16))  # 1.0 in fp16, 1.875 in bf16
+    scale = synthetic.default_scale()
+    if symbol.endswith("workspace_v3"):
+        ws = empty(torch, 16 * 8 * 130, "f32")
+        native.call(symbol, p(d_q), p(d_k), p(d_v), p(out), p(ws), p(d_len), 1, 1, capacity, 16, 2, 128, scale,
+                    stream.cuda_stream)
+    else:
+        native.call(symbol, p(d_q), p(d_k), p(d_v), p(out), 1, 1, capacity, 16, 2, 128, scale, p(d_len),
+                    stream.cuda_stream)
+    stream.synchronize()
+    assert not host(out).any()
+    assert not O.gqa(q, k, v, 0).any()
+
+
 @pytest.mark.parametrize("vocab,with_norm", [(151936, True), (1000, False), (1, True)])
 def test_lm_head_argmax(torch_gpu, native, stream, vocab, with_norm):
     torch = torch_gpu

@@ -1,0 +1,158 @@
+"""Every tensor a layer computes at the north-star tolerance (rel 1e-2 / abs 1e-3).
+
+The oracle (bit-equal to the GPU decode step, which the GPU tests check) is
+run one layer at a time: layer l alone, through a one-layer pointer table
+over the same weights and KV cache, with its input fed in as a one-row
+embedding table.  Chained over the 4 layers this reproduces the oracle's
+whole step bit for bit (checked against a HostModel stepping the same
+tokens).  Against the independent fp64 model of tests/_f64_decoder.py
+(values rounded to bf16 where the model stores bf16), 16 positions x 4
+layers:
+
+* every tensor a layer computes -- q and the new k / v rows (after RoPE),
+  the attention output, the o_proj output, the SwiGLU intermediate and the
+  down output, each from the oracle's own inputs to that op -- lies within
+  |got - want| <= 1e-3 + 1e-2 |want| element-wise, with no exception;
+* the residual stream is the exact bf16 sum of those outputs (the two
+  residual adds leave no freedom);
+* end to end (the fp64 layer on the same input and cache, its own
+  intermediates), the attention output and the layer output are within
+  1e-2 in relative L2 norm.  Element by element they are not, and cannot
+  be for bf16: rel 1e-2 is 2.56 bf16 ulps, a one-ulp difference in one
+  intermediate perturbs every later bf16 rounding (measured: 9 attention
+  flips become ~250 o_proj, ~5400 SwiGLU and ~950 layer-output flips of one
+  or two ulps), and a residual add that cancels turns an ulp of its
+  addends into a large relative error on a small result.  Measured worst
+  relative L2 error of a layer output: 0.0036.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from kudacuda_amd import synthetic
+from kudacuda_amd._native import QWEN2_MODEL_FIELDS
+from oracle import oracle as O
+from tests._f64_decoder import F64Decoder, bits
+from tests._host_model import HostModel
+
+SEED = 20260824
+LAYERS = 4
+STEPS = 16
+CAPACITY = 32
+ATOL, RTOL = 1.0e-3, 1.0e-2
+NO_LM_HEAD = 1 << 30  # prompt length that keeps the lm_head skipped
+
+
+class LayerRunner:
+    """Runs single layers of a HostModel through the oracle's decode step."""
+
+    def __init__(self, hm: HostModel) -> None:
+        self.hm = hm
+        self.embed = np.zeros((1, 2048), dtype=np.uint16)
+        self.tokens = np.zeros(CAPACITY, dtype=np.int32)
+        self.control = np.zeros(4, dtype=np.int32)
+        self.buffers = {n: np.zeros_like(getattr(hm, n)) for n in ("hidden", "query", "attn", "mlp")}
+        self.logits = np.zeros(1, dtype=np.uint16)
+        values = dict(zip(QWEN2_MODEL_FIELDS, hm.model_table))
+        values.update(embed=self.embed.ctypes.data, tokens=self.tokens.ctypes.data, control=self.control.ctypes.data,
+                      logits=self.logits.ctypes.data, **{n: b.ctypes.data for n, b in self.buffers.items()})
+        self.table = np.array([values[n] for n in QWEN2_MODEL_FIELDS], dtype=np.uint64)
+
+    def run(self, li: int, hidden_bits: np.ndarray, pos: int) -> dict[str, np.ndarray]:
+        self.embed[0] = hidden_bits
+        self.control[:] = [pos, NO_LM_HEAD, CAPACITY, 0]
+        O.qwen2_step(1, 1, self.hm.kv_capacity, self.hm.cfg.eps, self.hm.layer_table[li: li + 1], self.table)
+        return {n: b.copy() for n, b in self.buffers.items()}
+
+
+def _within(got_bits: np.ndarray, want_f64: np.ndarray) -> np.ndarray:
+    got = bits(got_bits)
+    return np.abs(got - want_f64) > ATOL + RTOL * np.abs(want_f64)
+
+
+@pytest.fixture(scope="module")
+def models():
+    layered = HostModel(SEED, num_layers=LAYERS, vocab=4096, kv_capacity=CAPACITY, token_capacity=CAPACITY)
+    whole = HostModel(SEED, num_layers=LAYERS, vocab=4096, kv_capacity=CAPACITY, token_capacity=CAPACITY)
+    return layered, whole, F64Decoder(layered)
+
+
+def _rb_sum(a_bits: np.ndarray, b_bits: np.ndarray) -> np.ndarray:
+    """bf16(a + b) of two bf16 vectors, as the kernels' residual add."""
+
+    return O.f32_to_bf16((bits(a_bits) + bits(b_bits)).astype(np.float32))
+
+
+def test_layer_outputs_within_the_north_star_tolerance(models):
+    layered, whole, ref = models
+    runner = LayerRunner(layered)
+    prompt = synthetic.prompt_ids(SEED + 5, STEPS + 1, 4096)
+    whole.reset(prompt)
+    checked = 0
+    flips = 0
+    worst_l2 = 0.0
+    for pos in range(STEPS):
+        hidden_bits = layered.embed[int(prompt[pos])].copy()
+        for li in range(LAYERS):
+            L = layered.layers[li]
+            past_k = bits(L["key_cache"][:, :pos].astype(np.uint32))
+            past_v = bits(L["value_cache"][:, :pos].astype(np.uint32))
+            end_to_end = ref.layer(li, bits(hidden_bits), pos, past_k, past_v)
+            got = runner.run(li, hidden_bits, pos)
+            k_row, v_row = L["key_cache"][:, pos].reshape(-1), L["value_cache"][:, pos].reshape(-1)
+            y1 = O.nf4_gemv2048(got["attn"], L["o_packed"], L["o_absmax"], 2048)
+            mid = _rb_sum(hidden_bits, y1)
+            y2 = O.down11008(got["mlp"], L["down_packed"], L["down_absmax"])
+            # the residual stream is the exact bf16 sum of the op outputs
+            assert np.array_equal(got["hidden"], _rb_sum(mid, y2)), (pos, li)
+            q_f, k_f, v_f = ref.qkv(li, bits(hidden_bits), pos)
+            keys = bits(L["key_cache"][:, : pos + 1].astype(np.uint32))
+            vals = bits(L["value_cache"][:, : pos + 1].astype(np.uint32))
+            ops = {
+                "query": (got["query"], q_f),
+                "k": (k_row, k_f),
+                "v": (v_row, v_f),
+                "attn": (got["attn"], ref.attention(bits(got["query"]), keys, vals)),
+                "o_proj": (y1, ref.o_proj(li, bits(got["attn"]))),
+                "mlp": (got["mlp"], ref.swiglu(li, bits(mid))),
+                "down": (y2, ref.down(li, bits(got["mlp"]))),
+            }
+            for name, (value, want) in ops.items():
+                bad = _within(value, want)
+                assert not bad.any(), (f"position {pos} layer {li} {name}: {int(bad.sum())} elements outside "
+                                       f"rel {RTOL} / abs {ATOL}")
+                checked += value.size
+            # end to end: tensor-level relative error of the layer's outputs
+            for name in ("attn", "hidden"):
+                diff = bits(got[name]) - end_to_end[name]
+                rel = float(np.linalg.norm(diff) / np.linalg.norm(end_to_end[name]))
+                assert rel <= RTOL, (pos, li, name, rel)
+                worst_l2 = max(worst_l2, rel)
+                flips += int(_within(got[name], end_to_end[name]).sum())
+            hidden_bits = got["hidden"]
+        whole.step()
+        # the chained single layers are the oracle's whole step
+        assert np.array_equal(hidden_bits, whole.hidden), pos
+        assert np.array_equal(runner.buffers["attn"], whole.attn), pos
+    assert checked == STEPS * LAYERS * (2048 + 2 * 256 + 2048 + 2048 + 11008 + 2048)
+    assert worst_l2 > 0.0  # the two restatements are genuinely different computations
+    print(f"end to end: worst relative L2 {worst_l2:.4f}; {flips} of {STEPS * LAYERS * 4096} attention/layer-output "
+          "elements outside the element-wise rule")
+
+
+def test_planted_layer_error_fails_the_tolerance(models):
+    # a mistake of one part in 50 in one attention output element (a dropped
+    # or doubled small term) must fail the per-element rule
+    layered, _, ref = models
+    hm = HostModel(SEED, num_layers=1, vocab=4096, kv_capacity=CAPACITY, token_capacity=CAPACITY)
+    runner = LayerRunner(hm)
+    hidden_bits = hm.embed[7].copy()
+    got = runner.run(0, hidden_bits, 0)
+    want = F64Decoder(hm).layer(0, bits(hidden_bits), 0)
+    assert not _within(got["attn"], want["attn"]).any()
+    i = int(np.argmax(np.abs(want["attn"])))
+    planted = got["attn"].copy()
+    planted[i] = O.f32_to_bf16(np.asarray([bits(planted[i:i + 1])[0] * 1.02], dtype=np.float32))[0]
+    assert _within(planted, want["attn"]).any()

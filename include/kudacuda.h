@@ -289,10 +289,17 @@ KUDACUDA_API void kudacuda_destroy(void* handle);
  *
  * All buffers are caller-owned; the model object keeps only the pointer
  * table.  layer_ptrs is [num_layers][KUDACUDA_QWEN2_LAYER_FIELDS], model_ptrs
- * is [KUDACUDA_QWEN2_MODEL_FIELDS] (indices below).  control is int32[4]:
+ * is [KUDACUDA_QWEN2_MODEL_FIELDS] (indices below).  control is int32[8]:
  * [0] step (= position of the current input token tokens[step]), [1] prompt
- * length, [2] token capacity of `tokens`; a step reads tokens[step], writes
- * tokens[step+1] once step+1 >= prompt length, then increments step.
+ * length, [2] token capacity of `tokens`, [3] stop token id (< 0: none),
+ * [4] done flag, [5] position of the stop token, [6..7] 0; a step reads
+ * tokens[step], writes tokens[step+1] once step+1 >= prompt length, then
+ * increments step.  A step that emits the stop token (the reference's EOS
+ * stop, tools/benchmark/benchmark_gemma.py:100-112,147, here decided on the
+ * device so no host sync per token is needed) keeps it in tokens[], sets
+ * [4] = 1 and [5] = its position; every later step is a no-op on the token
+ * array, the step counter and the KV cache, so a caller may replay a fixed
+ * number of steps and read [4] / [5] afterwards.
  * Counters (attention [2], lm_head [1], uint32) must be zero at creation. */
 enum {
     KUDACUDA_QWEN2_INPUT_NORM = 0,
@@ -329,7 +336,7 @@ enum {
     KUDACUDA_QWEN2_MLP,            /* bf16 [11008] */
     KUDACUDA_QWEN2_LOGITS,         /* bf16 [vocab] or 0 */
     KUDACUDA_QWEN2_TOKENS,         /* int32 [token capacity] */
-    KUDACUDA_QWEN2_CONTROL,        /* int32 [4] */
+    KUDACUDA_QWEN2_CONTROL,        /* int32 [8] */
     KUDACUDA_QWEN2_ATTN_PARTIALS,  /* fp32 [kudacuda_gqa_workspace_floats(kv_capacity)] */
     KUDACUDA_QWEN2_ATTN_COUNTERS,  /* uint32 [2] */
     KUDACUDA_QWEN2_LM_BEST,        /* fp32 [kudacuda_lm_head_workspace_floats()] */

@@ -69,6 +69,9 @@ struct Nf4RowsArgs {
     const float* rope_cos = nullptr;  // [capacity, 64]
     const float* rope_sin = nullptr;
     const int32_t* control = nullptr;  // control[0] = position of this token
+    // decode step only: the stop flag of the model's control block; when it
+    // is set the step writes no KV-cache row
+    const int32_t* done = nullptr;
     int64_t capacity = 0;
     uint16_t* kcache = nullptr;  // [2, capacity, 128]
     uint16_t* vcache = nullptr;
@@ -176,7 +179,7 @@ struct PrefillAttnArgs {
     float qk_scale_log2 = 0.0f;
 };
 hipError_t launch_prefill_attention(const PrefillAttnArgs& args, hipStream_t stream);
-// control[0] = step (one vector store; capture-safe)
+// control[0] = step, stop state cleared (control[4], control[5] = 0); capture-safe
 hipError_t launch_set_step(int32_t* control, int32_t step, hipStream_t stream);
 
 // Blockwise NF4 quantisation (blocksize 64) of n elements (n % 64 == 0).
@@ -235,8 +238,10 @@ struct LmHeadArgs {
     float* block_best = nullptr;      // [2 * grid] (value, index-as-bits)
     uint32_t* counter = nullptr;      // zero between calls
     int32_t* argmax_out = nullptr;    // receives the token id (may be null)
-    // decode bookkeeping (null for a plain lm_head call)
-    int32_t* control = nullptr;       // [0]=step [1]=prompt_len [2]=token capacity
+    // decode bookkeeping (null for a plain lm_head call): [0] step, [1]
+    // prompt length, [2] token capacity, [3] stop token id (< 0: none),
+    // [4] done flag, [5] position of the stop token once emitted
+    int32_t* control = nullptr;
     int32_t* tokens = nullptr;
 };
 hipError_t launch_lm_head_argmax(const LmHeadArgs& args, hipStream_t stream);

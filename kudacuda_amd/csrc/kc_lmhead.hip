@@ -15,7 +15,13 @@
 // skipped and the next prompt token stays in place; otherwise the winner is
 // written to tokens[step + 1]; step then advances.  This removes the host
 // argmax/.item() round trip the reference pays per token
-// (tools/benchmark/benchmark_gemma.py:328-352).
+// (tools/benchmark/benchmark_gemma.py:328-352).  Stop token (control[3] >= 0):
+// the step that emits it keeps it in tokens[], sets the done flag control[4]
+// and records its position in control[5]; from then on every step skips the
+// GEMV and neither writes a token nor advances -- the reference's EOS stop,
+// checked on the device so a host can replay many steps without a per-token
+// sync and read where the decode stopped
+// (tools/benchmark/benchmark_gemma.py:100-112,147).
 #include "kc_device.h"
 #include "kc_kernels.h"
 
@@ -55,9 +61,11 @@ __global__ __launch_bounds__(kLmThreads) void lm_head_kernel(LmHeadArgs a) {
 
     int32_t step = 0;
     bool active = true;
+    bool stopped = false;
     if (a.control != nullptr) {
         step = a.control[0];
-        active = step + 1 >= a.control[1];
+        stopped = a.control[4] != 0;
+        active = !stopped && step + 1 >= a.control[1];
     }
 
     float best = -__builtin_huge_valf();
@@ -232,10 +240,14 @@ __global__ __launch_bounds__(kLmThreads) void lm_head_kernel(LmHeadArgs a) {
         if (active && a.argmax_out != nullptr) {
             a.argmax_out[0] = best_idx;
         }
-        if (a.control != nullptr) {
+        if (a.control != nullptr && !stopped) {
             const int32_t next = step + 1;
             if (active && next < a.control[2]) {
                 a.tokens[next] = best_idx;
+            }
+            if (active && a.control[3] >= 0 && best_idx == a.control[3]) {
+                a.control[4] = 1;
+                a.control[5] = next;
             }
             a.control[0] = next;
         }

@@ -129,7 +129,7 @@ __device__ __forceinline__ Epi fetch_epilogue(const Nf4RowsArgs& a, const RowPai
 // holds d0/d1, lane 0 (and lane 1 for a GEMV pair) stores.
 template <typename T, RowMode MODE>
 __device__ __forceinline__ void row_epilogue(const Nf4RowsArgs& a, const RowPair& cur, const Epi& e, float d0,
-                                             float d1, int lane, int64_t pos) {
+                                             float d1, int lane, int64_t pos, bool write_cache) {
     if constexpr (MODE == RowMode::kGemv) {
         if (lane < 2 && (lane == 0 || cur.has1)) {
             const int64_t r = lane == 0 ? cur.r0 : cur.r1;
@@ -161,7 +161,7 @@ __device__ __forceinline__ void row_epilogue(const Nf4RowsArgs& a, const RowPair
                 if (m == 0) {
                     a.out[0][cur.r0] = T::store(o0);
                     a.out[0][cur.r1] = T::store(o1);
-                } else {
+                } else if (write_cache) {
                     uint16_t* cache = m == 1 ? a.kcache : a.vcache;
                     const int64_t g = cur.r0 >> 7;
                     const int64_t base = (g * a.capacity + pos) * 128;
@@ -209,9 +209,11 @@ __global__ __launch_bounds__(NTH) void nf4_rows2048_kernel(Nf4RowsArgs a, int64_
     const float2 pair_entry = pair_entry_fetch();
 
     int64_t pos = 0;
+    bool write_cache = true;
     if constexpr (MODE == RowMode::kQkvRope) {
         pos = a.control[0];
         pos = pos < 0 ? 0 : (pos >= a.capacity ? a.capacity - 1 : pos);
+        write_cache = a.done == nullptr || *a.done == 0;  // a stopped decode writes no cache row
     }
     const uint16_t* x = a.x;
     if (a.embed != nullptr) {
@@ -451,7 +453,7 @@ __global__ __launch_bounds__(NTH) void nf4_rows2048_kernel(Nf4RowsArgs a, int64_
             up = lane == i ? d1 : up;
             out_row = lane == i ? tasks[i].r0 : out_row;
         } else if (first + i * nwaves < ntasks) {
-            row_epilogue<T, MODE>(a, tasks[i], epi[i], d0, d1, lane, pos);
+            row_epilogue<T, MODE>(a, tasks[i], epi[i], d0, d1, lane, pos, write_cache);
         }
     }
     if constexpr (MODE == RowMode::kSwiGlu) {

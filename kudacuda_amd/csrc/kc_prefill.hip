@@ -747,9 +747,13 @@ __global__ __launch_bounds__(512) void prefill_attention_kernel(PrefillAttnArgs 
     }
 }
 
+// A prefill starts a generation: step = its last prompt position, stop state
+// cleared (control[4] done flag, control[5] stop position).
 __global__ void set_step_kernel(int32_t* control, int32_t step) {
     if (threadIdx.x == 0) {
         control[0] = step;
+        control[4] = 0;
+        control[5] = 0;
     }
 }
 

@@ -397,6 +397,7 @@ hipError_t model_op(const Model& m, int op, int64_t layer, bool bookkeeping, hip
             a.rope_cos = ptr<const float>(G[KUDACUDA_QWEN2_ROPE_COS]);
             a.rope_sin = ptr<const float>(G[KUDACUDA_QWEN2_ROPE_SIN]);
             a.control = ptr<const int32_t>(G[KUDACUDA_QWEN2_CONTROL]);
+            a.done = ptr<const int32_t>(G[KUDACUDA_QWEN2_CONTROL]) + 4;
             a.capacity = m.capacity;
             a.kcache = ptr<uint16_t>(L[KUDACUDA_QWEN2_KEY_CACHE]);
             a.vcache = ptr<uint16_t>(L[KUDACUDA_QWEN2_VALUE_CACHE]);

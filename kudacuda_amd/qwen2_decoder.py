@@ -90,7 +90,7 @@ class Qwen2Nf4Decoder:
             self.mlp = t.zeros(cfg.intermediate, dtype=t.bfloat16, device=device)
             self.logits = t.zeros(self.vocab, dtype=t.bfloat16, device=device)
             self.tokens = t.zeros(self.token_capacity, dtype=t.int32, device=device)
-            self.control = t.zeros(4, dtype=t.int32, device=device)
+            self.control = t.zeros(8, dtype=t.int32, device=device)
             self.attn_partials = t.zeros(int(lib.kudacuda_gqa_workspace_floats(self.kv_capacity)), dtype=t.float32,
                                          device=device)
             self.attn_counters = t.zeros(2, dtype=t.int32, device=device)
@@ -152,17 +152,28 @@ class Qwen2Nf4Decoder:
                    token_capacity=token_capacity, device=device, stream=stream)
 
     # ------------------------------------------------------------ running
-    def reset(self, prompt: np.ndarray, *, start_step: int = 0) -> None:
-        """Load prompt ids into the token array and set step/prompt/capacity."""
+    def reset(self, prompt: np.ndarray, *, start_step: int = 0, stop_token: int | None = None) -> None:
+        """Load prompt ids into the token array and set step/prompt/capacity.
+
+        With ``stop_token`` the device stops the decode at the step that emits
+        it (kept in the token array); later steps change nothing."""
 
         prompt = np.asarray(prompt, dtype=np.int32)
         if prompt.size < 1 or prompt.size > self.token_capacity:
             raise ValueError("prompt must have 1..token_capacity ids")
+        stop = -1 if stop_token is None else int(stop_token)
         t = self.torch
         with t.cuda.stream(self.stream):
             self.tokens[: prompt.size].copy_(t.from_numpy(prompt))
-            self.control.copy_(t.tensor([start_step, prompt.size, self.token_capacity, 0], dtype=t.int32))
+            self.control.copy_(t.tensor([start_step, prompt.size, self.token_capacity, stop, 0, 0, 0, 0],
+                                        dtype=t.int32))
         self.stream.synchronize()
+
+    def stopped_at(self) -> int | None:
+        """Position of the stop token in the token array, or None while running."""
+
+        control = self.control.cpu().numpy()
+        return int(control[5]) if int(control[4]) != 0 else None
 
     def set_step(self, step: int) -> None:
         t = self.torch
@@ -194,17 +205,22 @@ class Qwen2Nf4Decoder:
             for _ in range(steps):
                 self.step()
 
-    def generate(self, prompt: np.ndarray, new_tokens: int, *, graph: bool = True) -> np.ndarray:
-        """Greedy-decode ``new_tokens`` ids after ``prompt``; returns them."""
+    def generate(self, prompt: np.ndarray, new_tokens: int, *, graph: bool = True,
+                 stop_token: int | None = None) -> np.ndarray:
+        """Greedy-decode up to ``new_tokens`` ids after ``prompt``; returns
+        them, ending with ``stop_token`` if the decode emitted it.  The stop is
+        decided on the device: all steps are launched without a host sync."""
 
         prompt = np.asarray(prompt, dtype=np.int32)
         total = prompt.size + int(new_tokens)
         if total > min(self.token_capacity, self.kv_capacity + 1):
             raise ValueError("prompt + new tokens exceed the token/KV capacity")
-        self.reset(prompt)
+        self.reset(prompt, stop_token=stop_token)
         self.run_steps(total - 1, graph=graph)
         self.stream.synchronize()
-        return self.tokens[prompt.size:total].cpu().numpy().copy()
+        stop = self.stopped_at()
+        end = total if stop is None else stop + 1
+        return self.tokens[prompt.size:end].cpu().numpy().copy()
 
     def prefill(self, prompt: np.ndarray) -> None:
         """Load ``prompt`` and run it through the model in one multi-token pass

@@ -659,8 +659,16 @@ KCO_API void kco_qwen2_step(int64_t num_layers, int64_t vocab, int64_t capacity,
     const float qk_scale_log2 = (float)(1.0 / sqrt(128.0)) * kLog2e;
     int64_t plan[4];
     kco_gqa_plan(capacity, 0, plan);
+    /* a stopped decode (control[4]) writes no KV-cache row: the rows the QKV
+     * op writes at pos are put back before attention reads the cache */
+    const int stopped = control[4] != 0;
     for (int64_t layer = 0; layer < num_layers; ++layer) {
         const uint64_t* Lp = layer_ptrs + layer * L_FIELDS;
+        uint16_t saved[2][2][128];
+        for (int g = 0; g < 2 && stopped; ++g) {
+            memcpy(saved[0][g], P(uint16_t*, Lp[L_KEY_CACHE]) + ((int64_t)g * capacity + pos) * 128, 256);
+            memcpy(saved[1][g], P(uint16_t*, Lp[L_VALUE_CACHE]) + ((int64_t)g * capacity + pos) * 128, 256);
+        }
         kco_qkv_rope_cache(hidden, P(const uint16_t*, Lp[L_INPUT_NORM]), eps, P(const uint8_t*, Lp[L_Q_PACKED]),
                            P(const float*, Lp[L_Q_ABSMAX]), P(const uint16_t*, Lp[L_Q_BIAS]),
                            P(const uint8_t*, Lp[L_K_PACKED]), P(const float*, Lp[L_K_ABSMAX]),
@@ -668,6 +676,10 @@ KCO_API void kco_qwen2_step(int64_t num_layers, int64_t vocab, int64_t capacity,
                            P(const float*, Lp[L_V_ABSMAX]), P(const uint16_t*, Lp[L_V_BIAS]),
                            P(const float*, G[M_ROPE_COS]), P(const float*, G[M_ROPE_SIN]), pos, capacity, query,
                            P(uint16_t*, Lp[L_KEY_CACHE]), P(uint16_t*, Lp[L_VALUE_CACHE]));
+        for (int g = 0; g < 2 && stopped; ++g) {
+            memcpy(P(uint16_t*, Lp[L_KEY_CACHE]) + ((int64_t)g * capacity + pos) * 128, saved[0][g], 256);
+            memcpy(P(uint16_t*, Lp[L_VALUE_CACHE]) + ((int64_t)g * capacity + pos) * 128, saved[1][g], 256);
+        }
         kco_gqa(0, query, P(const uint16_t*, Lp[L_KEY_CACHE]), P(const uint16_t*, Lp[L_VALUE_CACHE]), capacity, L,
                 plan[0], plan[1], plan[2], qk_scale_log2, attn);
         kco_nf4_gemv2048(0, attn, P(const uint8_t*, Lp[L_O_PACKED]), P(const float*, Lp[L_O_ABSMAX]), NULL, hidden,
@@ -678,12 +690,20 @@ KCO_API void kco_qwen2_step(int64_t num_layers, int64_t vocab, int64_t capacity,
         kco_down11008(0, mlp, P(const uint8_t*, Lp[L_DOWN_PACKED]), P(const float*, Lp[L_DOWN_ABSMAX]), hidden, 2048,
                       hidden);
     }
+    /* bookkeeping: tokens[step + 1] once past the prompt; the stop token
+     * (control[3] >= 0) sets the done flag and its position, after which a
+     * step neither writes a token nor advances */
+    if (stopped) return;
     const int32_t step = control[0];
     const int active = step + 1 >= control[1];
     if (active) {
         const int32_t t = kco_lm_head_argmax(hidden, P(const uint16_t*, G[M_FINAL_NORM]), eps,
                                              P(const uint16_t*, G[M_EMBED]), vocab, P(uint16_t*, G[M_LOGITS]));
         if (step + 1 < control[2]) tokens[step + 1] = t;
+        if (control[3] >= 0 && t == control[3]) {
+            control[4] = 1;
+            control[5] = step + 1;
+        }
     }
     control[0] = step + 1;
 }

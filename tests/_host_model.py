@@ -43,7 +43,7 @@ class HostModel:
         self.mlp = np.zeros(11008, dtype=np.uint16)
         self.logits = np.zeros(vocab, dtype=np.uint16)
         self.tokens = np.zeros(token_capacity, dtype=np.int32)
-        self.control = np.zeros(4, dtype=np.int32)
+        self.control = np.zeros(8, dtype=np.int32)
         self._dummy = np.zeros(16, dtype=np.float32)
         self.layer_table = np.zeros((num_layers, len(QWEN2_LAYER_FIELDS)), dtype=np.uint64)
         for li, layer in enumerate(self.layers):
@@ -58,17 +58,19 @@ class HostModel:
         }
         self.model_table = np.array([values[n].ctypes.data for n in QWEN2_MODEL_FIELDS], dtype=np.uint64)
 
-    def reset(self, prompt: np.ndarray, start_step: int = 0) -> None:
+    def reset(self, prompt: np.ndarray, start_step: int = 0, stop_token: int | None = None) -> None:
         prompt = np.asarray(prompt, dtype=np.int32)
         self.tokens[: prompt.size] = prompt
-        self.control[:] = [start_step, prompt.size, self.token_capacity, 0]
+        self.control[:] = [start_step, prompt.size, self.token_capacity, -1 if stop_token is None else stop_token,
+                           0, 0, 0, 0]
 
     def step(self) -> None:
         O.qwen2_step(self.num_layers, self.vocab, self.kv_capacity, self.cfg.eps, self.layer_table, self.model_table)
 
-    def generate(self, prompt: np.ndarray, new_tokens: int) -> np.ndarray:
+    def generate(self, prompt: np.ndarray, new_tokens: int, stop_token: int | None = None) -> np.ndarray:
         prompt = np.asarray(prompt, dtype=np.int32)
-        self.reset(prompt)
+        self.reset(prompt, stop_token=stop_token)
         for _ in range(prompt.size + new_tokens - 1):
             self.step()
-        return self.tokens[prompt.size: prompt.size + new_tokens].copy()
+        end = int(self.control[5]) + 1 if self.control[4] else prompt.size + new_tokens
+        return self.tokens[prompt.size: end].copy()

@@ -3,7 +3,8 @@
 // 0 on success.
 //
 //   registry_smoke <code object>   load, resolve, launch through a descriptor,
-//                                  check, then the frozen and duplicate guards
+//                                  check, then the frozen, duplicate, missing-
+//                                  file and non-AMDGPU-file guards
 //   registry_smoke --no-device     on a host without a GPU: every call must
 //                                  report the missing device
 #include <hip/hip_runtime.h>
@@ -44,7 +45,7 @@ int no_device() {
     return 0;
 }
 
-int with_device(const char* path) {
+int with_device(const char* path, const char* self_path) {
     kudacuda::KudaCudaModuleRegistry registry(0);
     std::string error;
     if (registry.load("probe", path, &error) != 0) {
@@ -54,8 +55,13 @@ int with_device(const char* path) {
         return fail("duplicate load", error);
     }
     if (registry.load("other", "/nonexistent/none.hsaco", &error) != 1 ||
-        error.rfind("hipModuleLoad failed: ", 0) != 0) {
+        error != "code object is not readable: /nonexistent/none.hsaco") {
         return fail("load of a missing file", error);
+    }
+    // this program itself: an ELF file, but an x86-64 one
+    if (registry.load("host", self_path, &error) != 1 ||
+        error != std::string("not an AMDGPU code object (hipcc --genco): ") + self_path) {
+        return fail("load of a host executable", error);
     }
     hipFunction_t fn = nullptr;
     if (registry.resolve("probe", "kc_registry_probe_affine", &fn, &error) != 0 || fn == nullptr) {
@@ -69,8 +75,9 @@ int with_device(const char* path) {
         error != "module is not loaded: nope") {
         return fail("resolve in an unknown module", error);
     }
-    if (registry.resolve("probe", "kc_registry_probe_affine", &fn, &error) != 0) {
-        return fail("resolve again", error);
+    hipFunction_t again = nullptr;
+    if (registry.resolve("probe", "kc_registry_probe_affine", &again, &error) != 0 || again != fn) {
+        return fail("resolve again (the table's handle)", error);
     }
 
     const int n = 1000;
@@ -133,5 +140,5 @@ int main(int argc, char** argv) {
         std::fprintf(stderr, "usage: registry_smoke <code object> | --no-device\n");
         return 2;
     }
-    return with_device(argv[1]);
+    return with_device(argv[1], argv[0]);
 }

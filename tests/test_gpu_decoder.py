@@ -83,6 +83,55 @@ def test_generate_matches_oracle_tokens(small_pair):
     assert np.array_equal(gpu.generate(prompt, 24), cpu.generate(prompt, 24))
 
 
+@pytest.mark.parametrize("graph", [False, True])
+def test_stop_token_is_decided_on_the_device(small_pair, graph):
+    gpu, cpu = small_pair
+    prompt = synthetic.prompt_ids(SEED + 6, 6, 4096)
+    free = cpu.generate(prompt, 20)
+    k = next(i for i in range(2, 20) if free[i] not in free[:i])
+    stop = int(free[k])
+    got = gpu.generate(prompt, 20, graph=graph, stop_token=stop)  # all 25 steps launched, no host sync between
+    assert got.tolist() == free[: k + 1].tolist()
+    assert gpu.stopped_at() == prompt.size + k
+    assert np.array_equal(cpu.generate(prompt, 20, stop_token=stop), got)
+    assert np.array_equal(host(gpu.control), cpu.control)
+    # what this decode wrote (the host model's earlier unstopped run left
+    # more tokens and cache rows behind the stop position)
+    end = prompt.size + k
+    assert np.array_equal(host(gpu.tokens)[: end + 1], cpu.tokens[: end + 1])
+    for li in range(2):
+        assert np.array_equal(host(gpu.layers[li]["key_cache"])[:, :end], cpu.layers[li]["key_cache"][:, :end])
+    # more steps after the stop change nothing the decode owns
+    before = (host(gpu.tokens), host(gpu.control), host(gpu.layers[0]["value_cache"]), host(gpu.logits))
+    gpu.run_steps(5, graph=graph)
+    gpu.stream.synchronize()
+    after = (host(gpu.tokens), host(gpu.control), host(gpu.layers[0]["value_cache"]), host(gpu.logits))
+    assert all(np.array_equal(a, b) for a, b in zip(before, after))
+
+
+def test_prefill_emitting_the_stop_token_stops_the_decode(small_pair):
+    gpu, _ = small_pair
+    prompt = synthetic.prompt_ids(SEED + 7, 9, 4096)
+    gpu.prefill(prompt)
+    gpu.stream.synchronize()
+    first = int(host(gpu.tokens)[prompt.size])
+    gpu.reset(prompt, stop_token=first)
+    gpu.prefill(prompt)  # resets with no stop token, then emits `first` ...
+    gpu.stream.synchronize()
+    assert gpu.stopped_at() is None
+    gpu.reset(prompt, stop_token=first)
+    lib = gpu.native.lib
+    nbytes = int(lib.kudacuda_qwen2_prefill_workspace_bytes(prompt.size))
+    gpu.native.check(lib.kudacuda_qwen2_model_prefill(gpu.model, gpu._prefill_ws.data_ptr(), nbytes, 0, prompt.size,
+                                                      gpu.stream.cuda_stream), "prefill")
+    gpu.stream.synchronize()
+    assert gpu.stopped_at() == prompt.size  # ... and with the stop token set, the prefill's token stops it
+    tokens = host(gpu.tokens)
+    gpu.run_steps(3)
+    gpu.stream.synchronize()
+    assert int(host(gpu.control)[0]) == prompt.size and np.array_equal(host(gpu.tokens), tokens)
+
+
 @pytest.mark.parametrize("prompt_len,new,capacity", [(600, 24, 1024), (1030, 8, 2048)])
 def test_long_context_decode_matches_oracle(torch_gpu, native, prompt_len, new, capacity):
     # Decode-step attention past the short-context regime: at 600+ cached

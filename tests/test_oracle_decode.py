@@ -118,3 +118,26 @@ def test_oracle_reproduces_the_small_golden_fixture():
     assert prompt.tolist() == synthetic.prompt_ids(golden["seed"], prompt.size, golden["vocab"]).tolist()
     out = hm.generate(prompt, len(golden["tokens"]))
     assert out.tolist() == golden["tokens"]
+
+
+def test_stop_token_ends_the_decode_and_freezes_the_state():
+    # the reference stops greedy decoding at EOS, keeping the EOS token
+    # (tools/benchmark/benchmark_gemma.py:100-112,147); here the step that
+    # emits the stop token sets the done flag, later steps change nothing
+    golden = json.loads((GOLDEN / "decode_small_2l_v4096.json").read_text())
+    want = golden["tokens"]
+    k = next(i for i in range(3, len(want)) if want[i] not in want[:i])  # first token seen for the first time
+    hm = HostModel(golden["seed"], num_layers=golden["num_layers"], vocab=golden["vocab"],
+                   kv_capacity=golden["kv_capacity"], token_capacity=golden["kv_capacity"])
+    prompt = np.asarray(golden["prompt"], dtype=np.int32)
+    out = hm.generate(prompt, len(want), stop_token=want[k])
+    assert out.tolist() == want[: k + 1]
+    stop_pos = prompt.size + k
+    assert hm.control[4] == 1 and hm.control[5] == stop_pos and hm.control[0] == stop_pos
+    snapshot = (hm.tokens.copy(), hm.control.copy(), hm.layers[1]["key_cache"].copy(), hm.logits.copy())
+    for _ in range(3):
+        hm.step()
+    assert np.array_equal(hm.tokens, snapshot[0]) and np.array_equal(hm.control, snapshot[1])
+    assert np.array_equal(hm.layers[1]["key_cache"], snapshot[2]) and np.array_equal(hm.logits, snapshot[3])
+    # a stop token that never appears changes nothing
+    assert hm.generate(prompt, len(want), stop_token=golden["vocab"] + 5).tolist() == want

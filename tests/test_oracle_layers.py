@@ -52,7 +52,7 @@ class LayerRunner:
         self.hm = hm
         self.embed = np.zeros((1, 2048), dtype=np.uint16)
         self.tokens = np.zeros(CAPACITY, dtype=np.int32)
-        self.control = np.zeros(4, dtype=np.int32)
+        self.control = np.zeros(8, dtype=np.int32)
         self.buffers = {n: np.zeros_like(getattr(hm, n)) for n in ("hidden", "query", "attn", "mlp")}
         self.logits = np.zeros(1, dtype=np.uint16)
         values = dict(zip(QWEN2_MODEL_FIELDS, hm.model_table))
@@ -62,7 +62,7 @@ class LayerRunner:
 
     def run(self, li: int, hidden_bits: np.ndarray, pos: int) -> dict[str, np.ndarray]:
         self.embed[0] = hidden_bits
-        self.control[:] = [pos, NO_LM_HEAD, CAPACITY, 0]
+        self.control[:] = [pos, NO_LM_HEAD, CAPACITY, -1, 0, 0, 0, 0]
         O.qwen2_step(1, 1, self.hm.kv_capacity, self.hm.cfg.eps, self.hm.layer_table[li: li + 1], self.table)
         return {n: b.copy() for n, b in self.buffers.items()}
 

@@ -12,11 +12,18 @@ HBM, bracketed by stream synchronisation.  value = K / elapsed (tok/s).
 
 Also reported: per-kernel mean launch time from HIP events on the decode
 stream (each kernel launched back to back over all 36 layers, so weights are
-not cache resident), the roofline of the kernel that dominates the step, and
-the CPU oracle (oracle/kc_oracle.c, OpenMP) timed on a bounded sample of the
-same decode on this host, and the multi-token prefill of the same 64-token
-prompt (kudacuda_qwen2_model_prefill, HIP events, median of 5) beside the 63
-sequential decode steps the timed region starts after.
+not cache resident), the roofline of the kernel that dominates the step, the
+multi-token prefill of the same 64-token prompt (kudacuda_qwen2_model_prefill,
+HIP events, median of 5) beside the 63 sequential decode steps the timed
+region starts after, and ``per_config``: BASELINE configs 1-4 (NF4 GEMV,
+RMSNorm+QKV, SwiGLU MLP, GQA at 9 kv_lens) measured on the GPU
+(kudacuda_amd/opbench.py: captured launches over >256 MiB of distinct
+weights) with their HBM roofline, each beside the median of 20 calls of the
+same op in PyTorch on the host cores (oracle/torch_cpu.py, fp32, weights
+dequantised once).  cpu_baseline (config 5) is that PyTorch eager decoder
+(same model weights, fp32) timed on a bounded sample of decode steps on this
+host; cpu_baseline_oracle times the C oracle (oracle/kc_oracle.c, OpenMP) the
+same way.
 
 Usage: python bench.py [--gpus 1] [--steps 128] [--warmup 16]
 """
@@ -93,6 +100,88 @@ def _cpu_model() -> str:
     return f"{names[0]} ({len(names)} logical CPUs visible)" if names else "unknown"
 
 
+def torch_cpu_per_config(threads: int) -> dict[tuple[str, int], dict]:
+    """Median of 20 calls of each BASELINE config 1-4 op in PyTorch on the host
+    cores (fp32, weights dequantised once, excluded), keyed by (op, kv_len)."""
+
+    import torch
+
+    from oracle import torch_cpu as T
+
+    torch.set_num_threads(threads)
+    gen = torch.Generator().manual_seed(SEED)
+
+    def nf4(rows: int, cols: int) -> "torch.Tensor":
+        codes = torch.randint(0, 256, (rows * cols // 2,), dtype=torch.uint8, generator=gen)
+        absmax = torch.rand(rows * cols // 64, generator=gen) * 0.05 + 0.01
+        return T.dequantize(codes, absmax, rows, cols)
+
+    def vec(n: int, std: float = 1.0) -> "torch.Tensor":
+        return torch.randn(n, generator=gen) * std
+
+    sample = "median of 20 calls after 3 warm-up, torch CPU fp32, weights dequantised once (excluded)"
+    out: dict[tuple[str, int], dict] = {}
+
+    def record(op: str, us: float, kv_len: int = 0) -> None:
+        out[(op, kv_len)] = {"value": round(us, 2), "unit": "us/call", "cores": threads, "kind": "port",
+                             "impl": "PyTorch eager (oracle/torch_cpu.py)", "sample": sample}
+
+    w = nf4(2048, 2048)
+    x = vec(2048)
+    record("nf4_gemv_2048x2048", T.median_us(lambda: T.gemv(x, w)))
+    wq, wk, wv = nf4(2048, 2048), nf4(256, 2048), nf4(256, 2048)
+    bq, bk, bv, g = vec(2048, 0.01), vec(256, 0.01), vec(256, 0.01), vec(2048, 0.1) + 1
+    record("fused_rmsnorm_qkv_nf4", T.median_us(lambda: T.qkv(x, g, 1e-6, wq, bq, wk, bk, wv, bv)))
+    wg, wu, wd = nf4(11008, 2048), nf4(11008, 2048), nf4(2048, 11008)
+    record("mlp_nf4_gate_up_down", T.median_us(lambda: T.swiglu_mlp(x, g, 1e-6, wg, wu, wd)))
+    n = T.rmsnorm(x, g, 1e-6)
+    record("swiglu_nf4_gate_up", T.median_us(lambda: torch.nn.functional.silu(torch.mv(wg, n)) * torch.mv(wu, n)))
+    del w, wq, wk, wv, wg, wu, wd
+    scale = 1.0 / 128.0 ** 0.5
+    for kv_len in (1, 7, 128, 512, 585, 1024, 2048, 8192, 32768):
+        q, k, v = vec(16 * 128).reshape(16, 128), vec(2 * kv_len * 128).reshape(2, kv_len, 128), \
+            vec(2 * kv_len * 128).reshape(2, kv_len, 128)
+        record("gqa_decode_bf16", T.median_us(lambda: T.gqa(q, k, v, scale)), kv_len)
+    return out
+
+
+def torch_cpu_decode(layers: list[dict], embed_bits, final_norm_bits, prompt, seconds: float, threads: int) -> dict:
+    """Time the PyTorch eager decoder (oracle/torch_cpu.py) on the model's own
+    NF4 weights: consecutive decode steps from position 0 until ``seconds``."""
+
+    import torch
+
+    from oracle import torch_cpu as T
+
+    torch.set_num_threads(threads)
+    t0 = time.time()
+    dec = T.TorchCpuDecoder(layers, embed_bits, final_norm_bits, eps=synthetic_eps(), capacity=KV_BUCKET)
+    build_s = time.time() - t0
+    steps = 0
+    token = int(prompt[0])
+    t0 = time.perf_counter()
+    while True:
+        nxt = dec.step(token, steps)
+        steps += 1
+        token = int(prompt[steps]) if steps < len(prompt) else nxt
+        elapsed = time.perf_counter() - t0
+        if steps >= 2 and elapsed >= seconds:
+            break
+    return {
+        "value": round(steps / elapsed, 3), "unit": "tok/s", "cores": threads, "cpu": _cpu_model(), "kind": "port",
+        "impl": "PyTorch eager (oracle/torch_cpu.py): torch CPU fp32 ops over weights dequantised once",
+        "sample": f"{steps} decode steps (36 layers + tied lm_head + argmax, positions 0..{steps - 1}, the prompt "
+                  f"then its greedy continuation) of the benchmark model's own NF4 weights, {elapsed:.1f}s timed, "
+                  f"dequantisation {build_s:.0f}s excluded",
+    }
+
+
+def synthetic_eps() -> float:
+    from kudacuda_amd import synthetic
+
+    return float(synthetic.QWEN25_3B.eps)
+
+
 def cpu_baseline(seconds: float, threads: int) -> dict:
     """Time the oracle's decode step (same model, same math) on host cores."""
 
@@ -136,6 +225,7 @@ def main(argv: list[str] | None = None) -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-seconds", type=float, default=12.0)
     parser.add_argument("--op-iters", type=int, default=72)
+    parser.add_argument("--no-per-config", action="store_true", help="skip BASELINE configs 1-4")
     args = parser.parse_args(argv)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -272,12 +362,43 @@ def main(argv: list[str] | None = None) -> int:
         "token_parity_vs_oracle": parity,
         "reference_rtx3050_fp16_tok_s": 51.825,
     }
+    if not args.no_per_config:
+        from kudacuda_amd import opbench
+
+        print("[bench] BASELINE configs 1-4 on the GPU", file=sys.stderr, flush=True)
+        gpu_cases = opbench.collect(torch, (1, 2, 3, 4), launches=128)
+        print("[bench] BASELINE configs 1-4 in PyTorch on the CPU", file=sys.stderr, flush=True)
+        cpu_cases = torch_cpu_per_config(threads) if not args.no_cpu_baseline else {}
+        per_config = []
+        for case in gpu_cases:
+            entry = {"config": case["config"], "op": case["op"]}
+            if "kv_len" in case:
+                entry["kv_len"] = case["kv_len"]
+            entry.update(us=case["us"], bytes=case["bytes"],
+                         roofline={"bound": "hbm", "achieved": case["gbs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                   "frac": case["frac"]})
+            cpu = cpu_cases.get((case["op"], case.get("kv_len", 0)))
+            entry["cpu_baseline"] = cpu
+            if cpu is not None:
+                entry["speedup_vs_cpu"] = round(cpu["value"] / case["us"], 1)
+            per_config.append(entry)
+        result["per_config"] = per_config
     if not args.no_cpu_baseline:
-        print("[bench] timing CPU oracle baseline", file=sys.stderr, flush=True)
+        print("[bench] timing the PyTorch-CPU decoder baseline", file=sys.stderr, flush=True)
+        names = [f"{n}_{part}" for n in ("q", "k", "v", "o", "gate", "up", "down") for part in ("packed", "absmax")]
+        host_layers = [{n: layer[n].cpu() for n in names} | {n: layer[n].view(torch.int16).cpu().numpy().view(np.uint16)
+                                                            for n in ("q_bias", "k_bias", "v_bias", "input_norm",
+                                                                      "post_norm")} for layer in model.layers]
+        embed_bits = model.embed.view(torch.int16).cpu().numpy().view(np.uint16)
+        final_bits = model.final_norm.view(torch.int16).cpu().numpy().view(np.uint16)
         model.close()
         del model
         torch.cuda.empty_cache()
-        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds, threads)
+        result["cpu_baseline"] = torch_cpu_decode(host_layers, embed_bits, final_bits, prompt, args.cpu_seconds,
+                                                  threads)
+        del host_layers, embed_bits, final_bits
+        print("[bench] timing CPU oracle baseline", file=sys.stderr, flush=True)
+        result["cpu_baseline_oracle"] = cpu_baseline(args.cpu_seconds, threads)
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)

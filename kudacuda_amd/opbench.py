@@ -41,6 +41,8 @@ class Bench:
         self.stream = torch.cuda.Stream()
         self.launches = launches
         self.dev = "cuda:0"
+        self.results: list[dict[str, Any]] = []
+        self.echo = True
 
     def copies_for(self, nbytes: int) -> int:
         return max(1, min(self.launches, math.ceil(WORKING_SET / max(nbytes, 1))))
@@ -79,7 +81,9 @@ class Bench:
         line = {"op": op, "config": config, "us": round(us, 3), "bytes": nbytes, "gbs": round(gbs, 1),
                 "frac": round(gbs / PEAK_GBS, 4)}
         line.update(extra)
-        print(json.dumps(line), flush=True)
+        self.results.append(line)
+        if self.echo:
+            print(json.dumps(line), flush=True)
 
     # ---------------------------------------------------------------- configs
     def gemv(self) -> None:
@@ -188,6 +192,21 @@ class Bench:
             self.report("gqa_decode_bf16", 4, self.time(launch), nbytes, kv_len=length, copies=n)
             del caches
             self.torch.cuda.empty_cache()
+
+
+def collect(torch: Any, configs: tuple[int, ...] = (1, 2, 3, 4), launches: int = 128) -> list[dict[str, Any]]:
+    """Measure ``configs`` and return one result dict per case (no printing)."""
+
+    bench = Bench(torch, launches)
+    bench.echo = False
+    try:
+        with torch.cuda.stream(bench.stream):
+            for config in configs:
+                {1: bench.gemv, 2: bench.qkv, 3: bench.mlp, 4: bench.gqa, 6: bench.prefill_gemm}[config]()
+                torch.cuda.empty_cache()
+    finally:
+        bench.native.close()
+    return bench.results
 
 
 def main(argv: list[str] | None = None) -> int:

@@ -28,16 +28,17 @@ namespace kc {
 namespace {
 
 constexpr int kRowsThreads = 256;
-// gate/up blocks: 12 waves, of which waves 0..3 compute the shared norm and
-// waves 4..11 only read it (same arithmetic, fewer instructions per wave);
-// measured against 4, 8, 14 and 16 waves (9.07 / 8.75 / 8.50 / 9.84 /
-// 10.49 us): 12 waves keep two blocks per CU resident.
-constexpr int kSwiGluThreads = 768;
+// gate/up blocks: 11 waves, of which waves 0..3 compute the shared norm and
+// the rest only read it; 4 tasks per wave (kSwiGluWaves waves in all), so
+// ~251 blocks give about one block and 43 tasks per CU.  Measured in step
+// shape against 12-wave blocks of 2 tasks (8.76 -> 8.05 us) and 12-wave
+// blocks of 4 tasks (8.2 us).
+constexpr int kSwiGluThreads = 704;
+constexpr int64_t kSwiGluWaves = 2816;
 constexpr int kNormPitch = 36;  // floats per lane row of the shared norm (32 + 4: conflict-free)
-// Row-kernel launch cap: up to 6144 waves (24 per CU on 256 CUs), so a
-// wave owns at most 2 tasks of the 11008-task gate/up and the rest own 1;
-// measured faster than fewer waves with more tasks each (the dequant is
-// VALU-heavy and more resident waves hide its LDS and memory latency).
+// Launch cap of the other row kernels (GEMV, QKV): up to 6144 waves (24 per
+// CU on 256 CUs), one task per wave at the model's shapes; measured faster
+// than fewer waves with more tasks each there.
 constexpr int64_t kMaxRowWaves = 6144;
 
 // Decision points between adjacent codebook values: fp32 of the fp64
@@ -276,12 +277,13 @@ __global__ __launch_bounds__(NTH) void nf4_rows2048_kernel(Nf4RowsArgs a, int64_
         tasks[i] = map_task<MODE>(a, t < ntasks ? t : ntasks - 1);
         epi[i] = fetch_epilogue<T, MODE>(a, tasks[i], lane, pos);
     }
-    // Rows of the first kEarly tasks are requested up front, the rest one task
-    // at a time after the previous task's dots.  A wave whose load cannot be
-    // issued yet (the CU's memory queue is full while the launch's weights
-    // stream in) stalls in order, so gate/up waves that queue all their rows
-    // at once sit idle until the stream drains and then all compute together;
-    // issuing task i + 1 after task i's dots overlaps the two phases.
+    // Rows of the first kEarly tasks are requested up front.  Gate/up keeps
+    // one task in flight behind the current one: once task i's rows have
+    // arrived the wave requests task i + 1 and only then computes task i.  A
+    // wave whose load cannot be issued yet (the CU's memory queue is full
+    // while the launch's weights stream in) stalls in order, so requesting
+    // every task at once leaves the waves idle until the stream drains (and
+    // two tasks of lookahead measured slower than one: 8.67 vs 8.05 us).
     uint4 pk[TPW][2];
     float am[TPW][2];
     constexpr int kEarly = MODE == RowMode::kSwiGlu ? 1 : TPW;
@@ -434,7 +436,13 @@ __global__ __launch_bounds__(NTH) void nf4_rows2048_kernel(Nf4RowsArgs a, int64_
     int64_t out_row = tasks[0].r0;
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
-        if (i >= kEarly) {
+        if (MODE == RowMode::kSwiGlu && i + 1 < TPW) {
+            // the empty asm consumes task i's rows, so the wave waits for them here
+            asm volatile("" ::"v"(pk[i][0].x), "v"(pk[i][1].x), "v"(am[i][0]), "v"(am[i][1]));
+            __builtin_amdgcn_sched_barrier(0);
+            fetch_task(i + 1);
+            __builtin_amdgcn_sched_barrier(0);
+        } else if (MODE != RowMode::kSwiGlu && i >= kEarly) {
             __builtin_amdgcn_sched_barrier(0);
             fetch_task(i);
             __builtin_amdgcn_sched_barrier(0);
@@ -666,7 +674,8 @@ hipError_t launch_rows_t(const Nf4RowsArgs& a, hipStream_t stream) {
     }
     // every wave's tasks in flight at once
     const int64_t waves_per_block = (MODE == RowMode::kSwiGlu ? kSwiGluThreads : kRowsThreads) / 64;
-    int64_t tpw = (ntasks + kMaxRowWaves - 1) / kMaxRowWaves;
+    const int64_t max_waves = MODE == RowMode::kSwiGlu ? kSwiGluWaves : kMaxRowWaves;
+    int64_t tpw = (ntasks + max_waves - 1) / max_waves;
     tpw = tpw <= 1 ? 1 : (tpw <= 2 ? 2 : (tpw <= 4 ? 4 : 8));
     const int64_t waves = (ntasks + tpw - 1) / tpw;
     const int64_t blocks = (waves + waves_per_block - 1) / waves_per_block;

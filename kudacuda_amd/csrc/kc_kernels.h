@@ -25,33 +25,38 @@ enum class RowMode { kGemv = 0, kQkv = 1, kQkvRope = 2, kSwiGlu = 3 };
 // plan they were made with.  The attention kernel leaves them unmerged when
 // the split count at this kv_len is <= defer_max; its consumer merges them.
 constexpr int kGqaPartialStride = 130;
-constexpr int kGqaFlatTokens = 32;   // tokens per split on the flat path
-constexpr int kGqaMidTokens = 128;   // round-path tokens per split up to mid_max
-constexpr int kGqaMaxDefer = 8;      // most splits a consumer merges
+constexpr int kGqaRoundTokens = 32;      // tokens of one round (one per 16-lane group of a block)
+constexpr int64_t kGqaSplitCap = 256;    // most splits per KV head of an uncapped plan
+constexpr int kGqaMaxDefer = 8;          // most splits a consumer merges
+constexpr int kGqaMergeGroup = 16;       // merges sum splits in groups of this many, then the groups
+// Split cap of the decode step's plan: every split count it can reach is
+// merged by o_proj (deferred) or by the in-kernel ticket, so the step's graph
+// holds no merge-kernel node.
+constexpr int64_t kGqaStepSplits = 32;
 struct AttnSplits {
     const float* partials = nullptr;
     uint16_t* out = nullptr;  // optional: receives the merged vector (one block writes it)
     const int32_t* kv_len_device = nullptr;
     int32_t kv_len_offset = 0;
     int64_t capacity = 0;
-    int64_t chunk = 0;
-    int64_t flat_max = 0;
-    int64_t mid_max = 0;
+    int64_t split_cap = 0;
     int64_t max_splits = 0;
     int64_t defer_max = 0;
 };
 
-// Tokens per split at kv_len L: flat path (kGqaFlatTokens, one per group)
-// up to flat_max, flat path with two tokens per group up to 2 * flat_max
-// (the same number of splits at most), round path with kGqaMidTokens up to
-// mid_max and `chunk` beyond.
-__host__ __device__ inline int64_t gqa_split_tokens(int64_t L, int64_t flat_max, int64_t mid_max, int64_t chunk) {
-    return L <= flat_max ? kGqaFlatTokens
-                         : (L <= 2 * flat_max ? 2 * kGqaFlatTokens : (L <= mid_max ? kGqaMidTokens : chunk));
+// Tokens per split at kv_len L with at most split_cap splits: the fewest
+// whole rounds that keep the split count within the cap.  32-bit unsigned
+// arithmetic (kv_len and the cap are far below 2^31; the device has no
+// integer divider and a 64-bit quotient costs a long instruction loop).
+__host__ __device__ inline int64_t gqa_split_tokens(int64_t L, int64_t split_cap) {
+    const uint32_t rounds = (static_cast<uint32_t>(L) + kGqaRoundTokens - 1) / kGqaRoundTokens;
+    const uint32_t cap = static_cast<uint32_t>(split_cap);
+    const uint32_t per = (rounds + cap - 1) / cap;
+    return static_cast<int64_t>(kGqaRoundTokens) * (per > 1 ? per : 1);
 }
-__host__ __device__ inline int64_t gqa_split_count(int64_t L, int64_t flat_max, int64_t mid_max, int64_t chunk) {
-    const int64_t c = gqa_split_tokens(L, flat_max, mid_max, chunk);
-    return (L + c - 1) / c;
+__host__ __device__ inline int64_t gqa_split_count(int64_t L, int64_t split_cap) {
+    const uint32_t c = static_cast<uint32_t>(gqa_split_tokens(L, split_cap));
+    return static_cast<int64_t>((static_cast<uint32_t>(L) + c - 1) / c);
 }
 
 struct Nf4RowsArgs {
@@ -191,8 +196,8 @@ hipError_t launch_nf4_dequantize(const uint8_t* packed, const float* absmax, int
 
 // ------------------------------------------------------------------------ GQA
 // Split-KV grouped-query decode attention, 16 query heads / 2 KV heads /
-// head_dim 128.  `chunk` tokens per split (multiple of 64).  kv_len is read
-// from kv_len_device when non-null, else kv_len_host is used.
+// head_dim 128, gqa_split_tokens(kv_len, split_cap) tokens per split.  kv_len
+// is read from kv_len_device when non-null, else kv_len_host is used.
 struct GqaArgs {
     const uint16_t* q = nullptr;   // [16,128]
     const uint16_t* k = nullptr;   // [2, capacity, 128]
@@ -205,27 +210,23 @@ struct GqaArgs {
     int64_t kv_len_host = 0;
     int64_t capacity = 0;          // row stride of the cache
     int64_t max_splits = 0;        // grid size per KV head
-    int64_t chunk = 64;            // tokens per split on the round path
-    int64_t flat_max = 0;          // kv_len <= flat_max takes the flat path (kGqaFlatTokens per split)
-    int64_t mid_max = 0;           // flat_max < kv_len <= mid_max: round path, kGqaMidTokens per split
+    int64_t split_cap = 0;         // most splits at any kv_len (the split rule's parameter)
     int64_t defer_max = 0;         // <= kGqaMaxDefer: partials left for the consumer up to this many splits
     // 1..32: splits the partial kernel merges itself (merge kernel beyond).
-    // Measured: the merge kernel matches the ticket at 2-4 splits and beats
-    // it from ~9 (512 tokens: 11.1 -> 8.5 us), so standalone calls use 4.
-    int64_t ticket_max = 4;
+    // Measured on standalone calls: the ticket beats the merge kernel up to 16
+    // splits (8 splits: 7.5 vs 8.0 us, 16: 8.3 vs 8.5) and loses at 32 (11.1
+    // vs 8.9 us).
+    int64_t ticket_max = 16;
     float qk_scale_log2 = 0.0f;    // scale * log2(e)
 };
 hipError_t launch_gqa_decode(Act act, const GqaArgs& args, hipStream_t stream);
 // Split plan for a cache of `capacity` rows; split_limit > 0 caps the number
 // of splits (a caller-sized workspace).  Rule shared with the host oracle.
 struct GqaPlan {
-    int64_t chunk = 0;
-    int64_t flat_max = 0;
-    int64_t mid_max = 0;
-    int64_t max_splits = 0;
+    int64_t split_cap = 0;
+    int64_t max_splits = 0;  // the most splits any kv_len <= capacity needs: the grid
 };
 GqaPlan gqa_plan(int64_t capacity, int64_t split_limit);
-int64_t gqa_chunk_for(int64_t tokens);
 
 // ------------------------------------------------------------- lm_head/argmax
 struct LmHeadArgs {

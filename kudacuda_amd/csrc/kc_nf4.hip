@@ -301,7 +301,7 @@ __global__ __launch_bounds__(NTH) void nf4_rows2048_kernel(Nf4RowsArgs a, int64_
     bool merged = false;
     if constexpr (ATTN) {
         const int64_t L = attn_len < 0 ? 0 : (attn_len > a.attn.capacity ? a.attn.capacity : attn_len);
-        const int64_t nsplit = gqa_split_count(L, a.attn.flat_max, a.attn.mid_max, a.attn.chunk);
+        const int64_t nsplit = gqa_split_count(L, a.attn.split_cap);
         merged = nsplit >= 1 && nsplit <= a.attn.defer_max;
         if (merged) {
             float M = -__builtin_huge_valf();
@@ -667,7 +667,7 @@ hipError_t launch_rows_t(const Nf4RowsArgs& a, hipStream_t stream) {
         // the merge runs in the one-task-per-wave GEMV only
         const AttnSplits& at = a.attn;
         if (MODE != RowMode::kGemv || ntasks > kMaxRowWaves || a.gamma != nullptr || a.embed != nullptr ||
-            at.kv_len_device == nullptr || at.capacity <= 0 || at.chunk <= 0 || at.max_splits <= 0 ||
+            at.kv_len_device == nullptr || at.capacity <= 0 || at.split_cap <= 0 || at.max_splits <= 0 ||
             at.defer_max < 1 || at.defer_max > kGqaMaxDefer || at.defer_max > at.max_splits) {
             return hipErrorInvalidValue;
         }

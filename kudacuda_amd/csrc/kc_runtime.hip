@@ -148,9 +148,7 @@ int finish(Handle* h, const char* operation, hipError_t status) {
 void set_gqa_plan(GqaArgs& a, int64_t capacity, int64_t split_limit) {
     const GqaPlan p = gqa_plan(capacity, split_limit);
     a.capacity = capacity;
-    a.chunk = p.chunk;
-    a.flat_max = p.flat_max;
-    a.mid_max = p.mid_max;
+    a.split_cap = p.split_cap;
     a.max_splits = p.max_splits;
 }
 
@@ -419,7 +417,7 @@ hipError_t model_op(const Model& m, int op, int64_t layer, bool bookkeeping, hip
             a.counters = ptr<uint32_t>(G[KUDACUDA_QWEN2_ATTN_COUNTERS]);
             a.kv_len_device = ptr<const int32_t>(G[KUDACUDA_QWEN2_CONTROL]);
             a.kv_len_offset = 1;
-            set_gqa_plan(a, m.capacity, 0);
+            set_gqa_plan(a, m.capacity, kGqaStepSplits);
             a.defer_max = model_defer(a.max_splits);  // o_proj merges these
             // the rest by ticket: a merge kernel would be one more graph node
             // per layer even at the lengths that never need it
@@ -437,15 +435,13 @@ hipError_t model_op(const Model& m, int op, int64_t layer, bool bookkeeping, hip
             a.rows[0] = 2048;
             // attention output: merged here from the partials op 1 left
             GqaArgs plan;
-            set_gqa_plan(plan, m.capacity, 0);
+            set_gqa_plan(plan, m.capacity, kGqaStepSplits);
             a.attn.partials = ptr<const float>(G[KUDACUDA_QWEN2_ATTN_PARTIALS]);
             a.attn.out = ptr<uint16_t>(G[KUDACUDA_QWEN2_ATTN]);
             a.attn.kv_len_device = ptr<const int32_t>(G[KUDACUDA_QWEN2_CONTROL]);
             a.attn.kv_len_offset = 1;
             a.attn.capacity = plan.capacity;
-            a.attn.chunk = plan.chunk;
-            a.attn.flat_max = plan.flat_max;
-            a.attn.mid_max = plan.mid_max;
+            a.attn.split_cap = plan.split_cap;
             a.attn.max_splits = plan.max_splits;
             a.attn.defer_max = model_defer(plan.max_splits);
             return launch_nf4_rows2048(RowMode::kGemv, Act::kBf16, a, stream);
@@ -1226,7 +1222,9 @@ int kudacuda_qwen2_gqa_decode_vectorized(void* raw, uint64_t query, uint64_t key
                           {batch_size, query_len, query_heads, kv_heads, head_dim, scale}, kv_len, stream);
 }
 
-int64_t kudacuda_gqa_split_chunk(int64_t kv_tokens) { return kc::gqa_chunk_for(kv_tokens < 1 ? 1 : kv_tokens); }
+int64_t kudacuda_gqa_split_chunk(int64_t kv_tokens) {
+    return kc::gqa_split_tokens(kv_tokens < 1 ? 1 : kv_tokens, kc::kGqaSplitCap);
+}
 
 int64_t kudacuda_gqa_workspace_floats(int64_t kv_tokens) { return kc::gqa_workspace(kv_tokens < 1 ? 1 : kv_tokens); }
 

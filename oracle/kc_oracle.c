@@ -377,51 +377,34 @@ KCO_API void kco_down11008(int act, const uint16_t* x, const uint8_t* w, const f
 }
 
 /* ------------------------------------------------------------------- GQA */
-/* Block shape of the kernel: GQA_GROUPS groups of 16 lanes; a round covers
- * GQA_ROUND = 4 * GQA_GROUPS tokens (group gi takes base + 4gi + {0..3}). */
-#define GQA_GROUPS 32
-#define GQA_ROUND (4 * GQA_GROUPS)
+/* A block's 32 groups of 16 lanes take one token each per round. */
+#define GQA_ROUND 32
+/* most splits per KV head of an uncapped plan */
+#define GQA_SPLIT_CAP 256
+/* merges sum splits in groups of GQA_MERGE_GROUP, then the group sums */
+#define GQA_MERGE_GROUP 16
+/* Split cap of the decode step's plan (its merges are deferred or in-kernel). */
+#define GQA_STEP_SPLITS 32
 
-/* Flat path: kv_len <= flat_max, GQA_GROUPS tokens per split (one per group),
- * at most GQA_FLAT_SPLITS splits; kv_len <= 2 * flat_max, two tokens per
- * group (the same split count). */
-#define GQA_FLAT_SPLITS 32
-
-/* tokens per split on the round path for a cache of `tokens` rows */
-KCO_API int64_t kco_gqa_chunk_for(int64_t tokens) { (void)tokens; return 2 * GQA_ROUND; }
-
-/* Round path: GQA_ROUND-token splits up to GQA_MID_MAX, `chunk` beyond. */
-#define GQA_MID_MAX 8192
+/* tokens per split at kv_len L with at most split_cap splits: the fewest
+ * whole rounds that keep the split count within the cap */
+KCO_API int64_t kco_gqa_split_tokens(int64_t L, int64_t split_cap) {
+    const int64_t rounds = (L + GQA_ROUND - 1) / GQA_ROUND;
+    const int64_t per = (rounds + split_cap - 1) / split_cap;
+    return GQA_ROUND * (per > 1 ? per : 1);
+}
 
 /* The kernels' split plan for a cache of `capacity` rows (split_limit > 0 caps
- * every regime's splits): out = {chunk, flat_max, mid_max, max_splits}. */
+ * the splits): out = {split_cap, max_splits}. */
 KCO_API void kco_gqa_plan(int64_t capacity, int64_t split_limit, int64_t* plan) {
-    int64_t chunk = kco_gqa_chunk_for(capacity);
-    int64_t flat_splits = GQA_FLAT_SPLITS;
-    int64_t mid_max = GQA_MID_MAX;
-    if (split_limit > 0) {
-        if (split_limit < flat_splits) flat_splits = split_limit;
-        if (GQA_ROUND * split_limit < mid_max) mid_max = GQA_ROUND * split_limit;
-        const int64_t need = (capacity + split_limit - 1) / split_limit;
-        const int64_t rounded = (need + GQA_ROUND - 1) / GQA_ROUND * GQA_ROUND;
-        if (rounded > chunk) chunk = rounded;
-    }
-    int64_t flat_max = flat_splits * GQA_GROUPS;
-    if (flat_max > capacity) flat_max = capacity;
-    if (mid_max > capacity) mid_max = capacity;
-    const int64_t flat = (flat_max + GQA_GROUPS - 1) / GQA_GROUPS;
-    const int64_t mid = (mid_max + GQA_ROUND - 1) / GQA_ROUND;
-    const int64_t lng = (capacity + chunk - 1) / chunk;
-    int64_t ms = flat > mid ? flat : mid;
-    if (lng > ms) ms = lng;
-    plan[0] = chunk;
-    plan[1] = flat_max;
-    plan[2] = mid_max;
-    plan[3] = ms;
+    const int64_t cap = split_limit > 0 && split_limit < GQA_SPLIT_CAP ? split_limit : GQA_SPLIT_CAP;
+    const int64_t rounds = (capacity + GQA_ROUND - 1) / GQA_ROUND;
+    plan[0] = cap;
+    plan[1] = rounds < cap ? rounds : cap;
 }
 
 /* 16-lane partial dots of one K row with the 8 query heads of its group,
- * reduced by the DPP butterfly and scaled into the log2 domain. */
+ * reduced by the lanes' butterfly and scaled into the log2 domain. */
 static void gqa_scores(int act, const float qf[8][128], const uint16_t* krow, float qk_scale_log2, float* s8) {
     for (int hl = 0; hl < 8; ++hl) {
         float lanes[16];
@@ -434,14 +417,16 @@ static void gqa_scores(int act, const float qf[8][128], const uint16_t* krow, fl
     }
 }
 
-/* q [16,128], caches [2, capacity, 128], kv_len L; flat path for
- * L <= flat_max (GQA_GROUPS tokens per split) and L <= 2 * flat_max
- * (2 * GQA_GROUPS tokens per split), else the round path with
- * GQA_ROUND-token splits for L <= mid_max and `chunk`-token splits (a
- * multiple of GQA_ROUND) beyond. */
+/* q [16,128], caches [2, capacity, 128], kv_len L; split s of KV head g owns
+ * tokens [s*C, min(s*C + C, L)), C = kco_gqa_split_tokens(L, split_cap),
+ * processed in rounds of GQA_ROUND tokens with the online softmax:
+ * m' = max(m, round max), rescale r = exp2(m - m'), w_t = exp2(s_t - m'),
+ * l = l*r then + w_t in token order, acc = acc*r then fma(w_t, v_t, acc) in
+ * token order.  The split partials are merged with w_s = exp2(m_s - M) in
+ * groups of GQA_MERGE_GROUP splits (fma in split order), the group sums added
+ * in order. */
 KCO_API void kco_gqa(int act, const uint16_t* q, const uint16_t* kc, const uint16_t* vc, int64_t capacity,
-                     int64_t L, int64_t chunk, int64_t flat_max, int64_t mid_max, float qk_scale_log2,
-                     uint16_t* out) {
+                     int64_t L, int64_t split_cap, float qk_scale_log2, uint16_t* out) {
     if (L > capacity) L = capacity;
     if (L < 1) {
         /* empty cache: zero output (reference qwen2_gqa_workspace.cuh:118,
@@ -449,10 +434,8 @@ KCO_API void kco_gqa(int act, const uint16_t* q, const uint16_t* kc, const uint1
         memset(out, 0, sizeof(uint16_t) * 16 * 128);
         return;
     }
-    const int flat = L <= 2 * flat_max;
-    const int64_t tps = L <= flat_max ? GQA_GROUPS : 2 * GQA_GROUPS; /* flat tokens per split */
-    const int64_t C = L <= mid_max ? GQA_ROUND : chunk;
-    const int64_t nsplit = flat ? (L + tps - 1) / tps : (L + C - 1) / C;
+    const int64_t C = kco_gqa_split_tokens(L, split_cap);
+    const int64_t nsplit = (L + C - 1) / C;
     float* part = (float*)malloc(sizeof(float) * 16 * (size_t)nsplit * 130);
 #pragma omp parallel for collapse(2) schedule(static)
     for (int g = 0; g < 2; ++g) {
@@ -460,94 +443,43 @@ KCO_API void kco_gqa(int act, const uint16_t* q, const uint16_t* kc, const uint1
             float qf[8][128];
             for (int hl = 0; hl < 8; ++hl)
                 for (int d = 0; d < 128; ++d) qf[hl][d] = act_load(act, q[(8 * g + hl) * 128 + d]);
-            if (flat) {
-                /* one or two tokens per group; per head: M = max,
-                 * w_t = exp2(s_t - M), l = sum of w_t and acc = sum of w_t v_t,
-                 * both in token order */
-                const int64_t f0 = s * tps;
-                const int nvalid = (int)(f0 + tps < L ? tps : L - f0);
-                float sc[2 * GQA_GROUPS][8];
-                for (int t = 0; t < nvalid; ++t)
-                    gqa_scores(act, (const float(*)[128])qf, kc + ((int64_t)g * capacity + f0 + t) * 128,
+            float m[8], l[8], acc[8][128];
+            for (int hl = 0; hl < 8; ++hl) {
+                m[hl] = -INFINITY;
+                l[hl] = 0.0f;
+                for (int d = 0; d < 128; ++d) acc[hl][d] = 0.0f;
+            }
+            const int64_t t0 = s * C;
+            const int64_t tend = t0 + C < L ? t0 + C : L;
+            for (int64_t base = t0; base < tend; base += GQA_ROUND) {
+                const int nv = (int)(tend - base < GQA_ROUND ? tend - base : GQA_ROUND);
+                float sc[GQA_ROUND][8];
+                for (int t = 0; t < nv; ++t)
+                    gqa_scores(act, (const float(*)[128])qf, kc + ((int64_t)g * capacity + base + t) * 128,
                                qk_scale_log2, sc[t]);
                 for (int hl = 0; hl < 8; ++hl) {
-                    float M = -INFINITY;
-                    for (int t = 0; t < nvalid; ++t) M = fmaxf(M, sc[t][hl]);
-                    float w[2 * GQA_GROUPS];
-                    float lsum = 0.0f;
-                    for (int t = 0; t < nvalid; ++t) {
-                        w[t] = exp2_fixed(sc[t][hl] - M);
-                        lsum = lsum + w[t];
-                    }
-                    float* dst = part + ((int64_t)(8 * g + hl) * nsplit + s) * 130;
+                    float mr = -INFINITY;
+                    for (int t = 0; t < nv; ++t) mr = fmaxf(mr, sc[t][hl]);
+                    const float mn = fmaxf(m[hl], mr);
+                    const float r = exp2_fixed(m[hl] - mn);
+                    float w[GQA_ROUND];
+                    for (int t = 0; t < nv; ++t) w[t] = exp2_fixed(sc[t][hl] - mn);
+                    l[hl] = l[hl] * r;
+                    for (int t = 0; t < nv; ++t) l[hl] = l[hl] + w[t];
                     for (int d = 0; d < 128; ++d) {
-                        float acc = 0.0f;
-                        for (int t = 0; t < nvalid; ++t)
-                            acc = fmaf(w[t], act_load(act, vc[((int64_t)g * capacity + f0 + t) * 128 + d]), acc);
-                        dst[2 + d] = acc;
+                        float a = acc[hl][d] * r;
+                        for (int t = 0; t < nv; ++t)
+                            a = fmaf(w[t], act_load(act, vc[((int64_t)g * capacity + base + t) * 128 + d]), a);
+                        acc[hl][d] = a;
                     }
-                    dst[0] = M;
-                    dst[1] = lsum;
-                }
-                continue;
-            }
-            float gm[GQA_GROUPS][8], gl[GQA_GROUPS][8];
-            static __thread float gacc[GQA_GROUPS][8][128];
-            for (int gi = 0; gi < GQA_GROUPS; ++gi)
-                for (int hl = 0; hl < 8; ++hl) {
-                    gm[gi][hl] = -INFINITY;
-                    gl[gi][hl] = 0.0f;
-                    for (int d = 0; d < 128; ++d) gacc[gi][hl][d] = 0.0f;
-                }
-            const int64_t t0 = s * C;
-            const int64_t tend = (t0 + C < L) ? t0 + C : L;
-            for (int64_t base = t0; base < tend; base += GQA_ROUND) {
-                for (int gi = 0; gi < GQA_GROUPS; ++gi) {
-                    const int64_t tk = base + 4 * gi;
-                    int nvalid = (int)(tend - tk);
-                    nvalid = nvalid < 0 ? 0 : (nvalid > 4 ? 4 : nvalid);
-                    if (nvalid == 0) continue;
-                    float s2[4][8];
-                    for (int k = 0; k < nvalid; ++k)
-                        gqa_scores(act, (const float(*)[128])qf, kc + ((int64_t)g * capacity + tk + k) * 128,
-                                   qk_scale_log2, s2[k]);
-                    for (int hl = 0; hl < 8; ++hl) {
-                        float mt = -INFINITY;
-                        for (int k = 0; k < nvalid; ++k) mt = fmaxf(mt, s2[k][hl]);
-                        const float mnew = fmaxf(gm[gi][hl], mt);
-                        const float corr = exp2_fixed(gm[gi][hl] - mnew);
-                        gl[gi][hl] = gl[gi][hl] * corr;
-                        for (int d = 0; d < 128; ++d) gacc[gi][hl][d] = gacc[gi][hl][d] * corr;
-                        for (int k = 0; k < nvalid; ++k) {
-                            const float p = exp2_fixed(s2[k][hl] - mnew);
-                            gl[gi][hl] = gl[gi][hl] + p;
-                            const uint16_t* vrow = vc + ((int64_t)g * capacity + tk + k) * 128;
-                            for (int d = 0; d < 128; ++d)
-                                gacc[gi][hl][d] = fmaf(p, act_load(act, vrow[d]), gacc[gi][hl][d]);
-                        }
-                        gm[gi][hl] = mnew;
-                    }
+                    m[hl] = mn;
                 }
             }
             for (int hl = 0; hl < 8; ++hl) {
-                float M = -INFINITY;
-                for (int gi = 0; gi < GQA_GROUPS; ++gi) M = fmaxf(M, gm[gi][hl]);
                 float* dst = part + ((int64_t)(8 * g + hl) * nsplit + s) * 130;
-                float lsum = 0.0f;
-                for (int gi = 0; gi < GQA_GROUPS; ++gi) {
-                    if (gm[gi][hl] == -INFINITY) continue;
-                    lsum = fmaf(gl[gi][hl], exp2_fixed(gm[gi][hl] - M), lsum);
-                }
-                for (int d = 0; d < 128; ++d) {
-                    float av = 0.0f;
-                    for (int gi = 0; gi < GQA_GROUPS; ++gi) {
-                        if (gm[gi][hl] == -INFINITY) continue;
-                        av = fmaf(gacc[gi][hl][d], exp2_fixed(gm[gi][hl] - M), av);
-                    }
-                    dst[2 + d] = av;
-                }
-                dst[0] = M;
-                dst[1] = lsum;
+                dst[0] = m[hl];
+                dst[1] = l[hl];
+                memcpy(dst + 2, acc[hl], sizeof(float) * 128);
             }
         }
     }
@@ -557,11 +489,21 @@ KCO_API void kco_gqa(int act, const uint16_t* q, const uint16_t* kc, const uint1
         for (int64_t s = 0; s < nsplit; ++s) M = fmaxf(M, src[s * 130]);
         for (int d = 0; d < 128; ++d) {
             float lt = 0.0f, o = 0.0f;
-            for (int64_t s = 0; s < nsplit; ++s) {
-                const float* p = src + s * 130;
-                const float w = exp2_fixed(p[0] - M);
-                lt = fmaf(p[1], w, lt);
-                o = fmaf(p[2 + d], w, o);
+            for (int64_t j = 0; j < nsplit; j += GQA_MERGE_GROUP) {
+                float lg = 0.0f, og = 0.0f;
+                for (int64_t s = j; s < j + GQA_MERGE_GROUP && s < nsplit; ++s) {
+                    const float* p = src + s * 130;
+                    const float w = exp2_fixed(p[0] - M);
+                    lg = fmaf(p[1], w, lg);
+                    og = fmaf(p[2 + d], w, og);
+                }
+                if (j == 0) {
+                    lt = lg;
+                    o = og;
+                } else {
+                    lt = lt + lg;
+                    o = o + og;
+                }
             }
             out[h * 128 + d] = act_store(act, o / lt);
         }
@@ -657,8 +599,8 @@ KCO_API void kco_qwen2_step(int64_t num_layers, int64_t vocab, int64_t capacity,
     int64_t L = (int64_t)control[0] + 1;
     if (L > capacity) L = capacity;
     const float qk_scale_log2 = (float)(1.0 / sqrt(128.0)) * kLog2e;
-    int64_t plan[4];
-    kco_gqa_plan(capacity, 0, plan);
+    int64_t plan[2];
+    kco_gqa_plan(capacity, GQA_STEP_SPLITS, plan);
     /* a stopped decode (control[4]) writes no KV-cache row: the rows the QKV
      * op writes at pos are put back before attention reads the cache */
     const int stopped = control[4] != 0;
@@ -681,7 +623,7 @@ KCO_API void kco_qwen2_step(int64_t num_layers, int64_t vocab, int64_t capacity,
             memcpy(P(uint16_t*, Lp[L_VALUE_CACHE]) + ((int64_t)g * capacity + pos) * 128, saved[1][g], 256);
         }
         kco_gqa(0, query, P(const uint16_t*, Lp[L_KEY_CACHE]), P(const uint16_t*, Lp[L_VALUE_CACHE]), capacity, L,
-                plan[0], plan[1], plan[2], qk_scale_log2, attn);
+                plan[0], qk_scale_log2, attn);
         kco_nf4_gemv2048(0, attn, P(const uint8_t*, Lp[L_O_PACKED]), P(const float*, Lp[L_O_ABSMAX]), NULL, hidden,
                          2048, hidden);
         kco_swiglu(0, hidden, P(const uint16_t*, Lp[L_POST_NORM]), eps, P(const uint8_t*, Lp[L_GATE_PACKED]),

@@ -72,11 +72,11 @@ def lib() -> ctypes.CDLL:
                                      _f32, _f32, _i64, _i64, _u16, _u16, _u16]
     L.kco_swiglu.argtypes = [ctypes.c_int, _u16, _vp, _f, _u8, _f32, _u8, _f32, _i64, _u16]
     L.kco_down11008.argtypes = [ctypes.c_int, _u16, _u8, _f32, _vp, _i64, _u16]
-    L.kco_gqa_chunk_for.argtypes = [_i64]
-    L.kco_gqa_chunk_for.restype = _i64
+    L.kco_gqa_split_tokens.argtypes = [_i64, _i64]
+    L.kco_gqa_split_tokens.restype = _i64
     L.kco_gqa_plan.argtypes = [_i64, _i64, ctypes.c_void_p]
     L.kco_gqa_plan.restype = None
-    L.kco_gqa.argtypes = [ctypes.c_int, _u16, _u16, _u16, _i64, _i64, _i64, _i64, _i64, _f, _u16]
+    L.kco_gqa.argtypes = [ctypes.c_int, _u16, _u16, _u16, _i64, _i64, _i64, _f, _u16]
     L.kco_lm_head_argmax.argtypes = [_u16, _vp, _f, _u16, _i64, _vp]
     L.kco_lm_head_argmax.restype = ctypes.c_int32
     L.kco_qwen2_step.argtypes = [_i64, _i64, _i64, _f, _vp, _vp]
@@ -210,37 +210,38 @@ def down11008(h, packed, absmax, *, residual=None, rows: int = 2048, dtype: str 
     return out
 
 
-def gqa_chunk_for(tokens: int) -> int:
-    return int(lib().kco_gqa_chunk_for(int(tokens)))
+GQA_STEP_SPLITS = 32  # split cap of the decode step's plan
 
 
-def gqa_plan(capacity: int, split_limit: int = 0) -> tuple[int, int, int, int]:
-    """(chunk, flat_max, mid_max, max_splits) of the kernels for a cache of `capacity` rows."""
+def gqa_split_tokens(kv_len: int, split_cap: int) -> int:
+    """Tokens per split at kv_len with at most split_cap splits (whole 32-token rounds)."""
 
-    plan = np.zeros(4, dtype=np.int64)
+    return int(lib().kco_gqa_split_tokens(int(kv_len), int(split_cap)))
+
+
+def gqa_plan(capacity: int, split_limit: int = 0) -> tuple[int, int]:
+    """(split_cap, max_splits) of the kernels for a cache of `capacity` rows."""
+
+    plan = np.zeros(2, dtype=np.int64)
     lib().kco_gqa_plan(int(capacity), int(split_limit), plan.ctypes.data)
-    return int(plan[0]), int(plan[1]), int(plan[2]), int(plan[3])
+    return int(plan[0]), int(plan[1])
 
 
-def gqa(q, kcache, vcache, kv_len: int, *, chunk: int | None = None, flat_max: int | None = None,
-        mid_max: int | None = None, split_limit: int = 0, scale: float | None = None,
-        dtype: str = "bf16") -> np.ndarray:
+def gqa(q, kcache, vcache, kv_len: int, *, split_cap: int | None = None, split_limit: int = 0,
+        scale: float | None = None, dtype: str = "bf16") -> np.ndarray:
     """Split-KV GQA decode (16 q heads, 2 kv heads, d 128), caches [2, cap, 128].
 
-    chunk / flat_max / mid_max default to the kernels' plan for the cache's
-    capacity (split_limit as for a caller-sized workspace); flat_max=0 forces
-    the round path, mid_max=0 its `chunk`-token splits."""
+    split_cap defaults to the kernels' plan for the cache's capacity
+    (split_limit as for a caller-sized workspace, GQA_STEP_SPLITS for the
+    decode step); split_cap=1 is one split of every token."""
 
     capacity = kcache.shape[1]
-    plan_chunk, plan_flat, plan_mid, _ = gqa_plan(capacity, split_limit)
-    chunk = plan_chunk if chunk is None else chunk
-    flat_max = plan_flat if flat_max is None else flat_max
-    mid_max = plan_mid if mid_max is None else mid_max
+    split_cap = gqa_plan(capacity, split_limit)[0] if split_cap is None else split_cap
     scale = np.float32(1.0 / math.sqrt(128.0)) if scale is None else np.float32(scale)
     qk = np.float32(scale * LOG2E_F32)
     out = np.zeros(2048, dtype=np.uint16)
     lib().kco_gqa(_act(dtype), np.ascontiguousarray(q), np.ascontiguousarray(kcache), np.ascontiguousarray(vcache),
-                  capacity, kv_len, chunk, flat_max, mid_max, float(qk), out)
+                  capacity, kv_len, split_cap, float(qk), out)
     return out
 
 

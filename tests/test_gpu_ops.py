@@ -193,10 +193,11 @@ def test_mlp_config3(torch_gpu, native, stream, with_norm, with_residual):
     _close(host(out), y)
 
 
-# flat path up to 512 (edges 32/33, 511/512); round path beyond with
-# 128-token splits up to 8192 (ticket merge up to 2048 = 16 splits, merge
-# kernel from 2049) and 256-token splits past it (8193, 32768)
-KV_LENS = [1, 7, 32, 33, 37, 128, 511, 512, 513, 585, 1024, 2048, 2049, 8192, 8193, 32768]
+# one-round (32-token) splits up to 8192 tokens: finished in place up to 32,
+# ticket merge up to 4 splits (128), merge kernel beyond, with one merge group
+# up to 512 and more past it; splits of 2, 3 and 4 rounds past 8192, 16384
+# and 24576 tokens (256 splits per KV head at 32768)
+KV_LENS = [1, 7, 32, 33, 37, 128, 129, 511, 512, 513, 585, 1024, 2048, 2049, 8192, 8193, 16385, 32768]
 
 
 @pytest.mark.parametrize("kv_len", KV_LENS)
@@ -219,7 +220,8 @@ def test_gqa_decode_bf16_config4(torch_gpu, native, stream, kv_len):
 
 
 @pytest.mark.parametrize("kv_len,capacity", [(1, 512), (100, 512), (512, 512), (33, 2048), (513, 2048), (585, 2048),
-                                             (2048, 2048), (200, 32768), (8000, 32768)])
+                                             (2048, 2048), (200, 32768), (8000, 32768), (8193, 32768),
+                                             (30001, 32768)])
 def test_gqa_graph_reads_device_kv_len(torch_gpu, native, stream, kv_len, capacity):
     torch = torch_gpu
     q, k, v = synthetic.gqa_inputs(SEED, kv_len, capacity)
@@ -230,7 +232,7 @@ def test_gqa_graph_reads_device_kv_len(torch_gpu, native, stream, kv_len, capaci
     native.call("kudacuda_qwen2_gqa_decode_graph_bf16", p(d_q), p(d_k), p(d_v), p(out), 1, 1, capacity, 16, 2, 128,
                 scale, p(d_len), stream.cuda_stream)
     stream.synchronize()
-    assert np.array_equal(host(out), O.gqa(q, k, v, kv_len, chunk=O.gqa_chunk_for(capacity)))
+    assert np.array_equal(host(out), O.gqa(q, k, v, kv_len))
 
 
 @pytest.mark.parametrize("symbol", ["kudacuda_qwen2_gqa_decode", "kudacuda_qwen2_gqa_decode_group_tiled",
@@ -260,10 +262,10 @@ def test_gqa_workspace_v3(torch_gpu, native, stream):
     capacity = 512
     scale = synthetic.default_scale()
     ws = empty(torch, 16 * 8 * 130, "f32")
-    # reference tests/qwen2_gqa_workspace_smoke.cu:29-49, plus the edges of the
-    # flat path under this 8-split workspace (256: one token per group; 257 and
-    # 512: two tokens per group)
-    for kv_len in (1, 7, 64, 128, 256, 257, 512):
+    # reference tests/qwen2_gqa_workspace_smoke.cu:29-49, plus the edges of
+    # this 8-split workspace's rule (up to 256 tokens one-round splits, then
+    # two-round splits)
+    for kv_len in (1, 7, 64, 128, 256, 257, 300, 511, 512):
         q, k, v = synthetic.gqa_inputs(SEED + kv_len, kv_len, capacity)
         q16 = O.f32_to_f16(O.bf16_to_f32(q))
         k16 = O.f32_to_f16(O.bf16_to_f32(k)).reshape(2, capacity, 128)

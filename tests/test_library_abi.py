@@ -72,7 +72,7 @@ def test_null_handle_fails_closed(lib):
 
 
 def test_workspace_size_helpers(lib):
-    assert lib.kudacuda_gqa_split_chunk(2048) == 256
+    assert lib.kudacuda_gqa_split_chunk(2048) == 32 and lib.kudacuda_gqa_split_chunk(32768) == 128
     floats = lib.kudacuda_gqa_workspace_floats(2048)
     assert floats >= 16 * 8 * 130
     assert lib.kudacuda_lm_head_workspace_floats() >= 2

@@ -68,14 +68,18 @@ def test_identical_keys_average_the_values():
         assert np.all(np.abs(out[h] - mean[h // 8]) <= 2.0 ** -8 * np.abs(mean[h // 8]) + 1e-5)
 
 
-@pytest.mark.parametrize("chunk", [128, 256, 512, 1024])
-def test_split_size_changes_only_rounding(chunk):
+@pytest.mark.parametrize("split_cap", [1, 2, 4, 16, 63])
+def test_split_size_changes_only_rounding(split_cap):
+    """Caps 1..63 at 2000 tokens give splits of 63, 32, 16, 4 and 1 rounds
+    (one split of every token, down to 32-token splits); each is the same
+    attention up to fp32 rounding."""
+
     rng = np.random.default_rng(6)
     kv_len = 2000
     q = O.f32_to_bf16(rng.standard_normal(2048).astype(F))
     k = O.f32_to_bf16(rng.standard_normal((2, 2048, 128)).astype(F))
     v = O.f32_to_bf16(rng.standard_normal((2, 2048, 128)).astype(F))
-    got = O.bf16_to_f32(O.gqa(q, k, v, kv_len, chunk=chunk, mid_max=0))
+    got = O.bf16_to_f32(O.gqa(q, k, v, kv_len, split_cap=split_cap))
     want = gqa_f64(O.bf16_to_f32(q), O.bf16_to_f32(k), O.bf16_to_f32(v), kv_len, SCALE)
     assert np.all(np.abs(got - want) <= 2.0 ** -7 * np.abs(want) + 2e-4)
 
@@ -89,60 +93,99 @@ def test_planted_wrong_group_mapping_fails():
     assert np.abs(got - want).max() > tol
 
 
-def test_split_plan_covers_every_regime():
-    # (chunk, flat_max, mid_max, max_splits): flat path with 32-token splits up
-    # to 32 x 32 tokens (8 x 32 with the reference's 16 x 8 x 130 workspace),
-    # round path with 128-token splits up to 8192 tokens, 256-token beyond
-    assert O.gqa_plan(2048) == (256, 1024, 2048, 32)
-    assert O.gqa_plan(32768) == (256, 1024, 8192, 128)
-    assert O.gqa_plan(65536) == (256, 1024, 8192, 256)
-    assert O.gqa_plan(100) == (256, 100, 100, 4)
-    assert O.gqa_plan(512, split_limit=8) == (256, 256, 512, 8)
-    assert O.gqa_plan(1) == (256, 1, 1, 1)
-    # a capped workspace also caps the long splits' count
-    chunk, _, mid_max, splits = O.gqa_plan(32768, split_limit=8)
-    assert splits == 8 and chunk * 8 >= 32768 and mid_max == 1024
+def test_split_plan():
+    # (split_cap, max_splits): up to 256 splits per KV head, 32-token rounds;
+    # a caller-sized workspace caps the splits
+    assert O.gqa_plan(2048) == (256, 64)
+    assert O.gqa_plan(32768) == (256, 256)
+    assert O.gqa_plan(65536) == (256, 256)
+    assert O.gqa_plan(100) == (256, 4)
+    assert O.gqa_plan(512, split_limit=8) == (8, 8)
+    assert O.gqa_plan(1) == (256, 1)
+    assert O.gqa_plan(2048, split_limit=O.GQA_STEP_SPLITS) == (32, 32)
+    # one-round splits up to 256 rounds, then the fewest rounds per split
+    assert [O.gqa_split_tokens(n, 256) for n in (1, 8192, 8193, 16384, 16385, 32768, 65536)] == \
+        [32, 32, 64, 64, 96, 128, 256]
+    # the decode step: one round per split up to 1024 tokens
+    assert [O.gqa_split_tokens(n, 32) for n in (1024, 1025, 2048, 2049)] == [32, 64, 64, 96]
 
 
+@pytest.mark.parametrize("cap", [1, 3, 8, 32, 256])
+def test_split_rule_is_the_fewest_whole_rounds_within_the_cap(cap):
+    for n in range(1, 9000, 7):
+        c = O.gqa_split_tokens(n, cap)
+        assert c % 32 == 0 and -(-n // c) <= cap, (n, c)
+        assert c == 32 or -(-n // (c - 32)) > cap, (n, c)  # one round fewer breaks the cap
+
+
+@pytest.mark.parametrize("split_cap", [None, O.GQA_STEP_SPLITS, 3])
 @pytest.mark.parametrize("kv_len", [31, 32, 33, 200, 1023, 1024, 1025, 1087, 2047, 2048, 2049, 2100])
-def test_flat_path_boundaries_match_fp64(kv_len):
-    """Split edges of the flat path (a full split, a one-token split, the
-    32-split maximum), of its two-token-per-group form (64-token splits up to
-    2048 tokens) and the first lengths past it (round path, 128-token
-    splits)."""
+def test_split_edges_match_fp64(kv_len, split_cap):
+    """Round and split edges (a full round, a one-token round, 16 / 17 splits
+    on either side of a merge group, the decode step's one-round limit at
+    1024 tokens and its two-round splits past it, splits of many rounds with
+    cap 3)."""
 
     rng = np.random.default_rng([7, kv_len])
     q = O.f32_to_bf16(rng.standard_normal(2048).astype(F))
     k = O.f32_to_bf16(rng.standard_normal((2, 2100, 128)).astype(F))
     v = O.f32_to_bf16(rng.standard_normal((2, 2100, 128)).astype(F))
-    got = O.bf16_to_f32(O.gqa(q, k, v, kv_len))
+    got = O.bf16_to_f32(O.gqa(q, k, v, kv_len, split_cap=split_cap))
     want = gqa_f64(O.bf16_to_f32(q), O.bf16_to_f32(k), O.bf16_to_f32(v), kv_len, SCALE)
     assert np.all(np.abs(got - want) <= 2.0 ** -8 * np.abs(want) + 2e-4)
 
 
 @pytest.mark.parametrize("kv_len", [1, 7, 64, 128, 512])
-@pytest.mark.parametrize("regime", [dict(flat_max=0), dict(flat_max=0, mid_max=0)])
-def test_round_path_at_short_lengths_matches_the_workspace_fixture(kv_len, regime):
-    """flat_max=0 forces the round path with 128-token splits (what a capped
-    workspace uses past its flat limit), mid_max=0 too its 256-token splits;
-    the reference fixture's tolerance holds for both."""
+@pytest.mark.parametrize("split_cap", [1, 2])
+def test_many_round_splits_match_the_workspace_fixture(kv_len, split_cap):
+    """Caps of one and two splits make every length past a round a split of
+    several rounds (the online rescale between rounds); the reference
+    fixture's tolerance holds."""
 
     q, k, v, lens, tol = _kat.gqa_workspace_case()
-    got = O.f16_to_f32(O.gqa(q, k, v, kv_len, dtype="f16", **regime))
+    got = O.f16_to_f32(O.gqa(q, k, v, kv_len, dtype="f16", split_cap=split_cap))
     want = gqa_f64(O.f16_to_f32(q), O.f16_to_f32(k), O.f16_to_f32(v), kv_len, SCALE)
     assert np.abs(got - want).max() <= tol
 
 
-def test_flat_and_round_paths_agree():
+def test_one_round_and_many_round_splits_agree():
     rng = np.random.default_rng(9)
     kv_len = 300
     q = O.f32_to_bf16(rng.standard_normal(2048).astype(F))
     k = O.f32_to_bf16(rng.standard_normal((2, kv_len, 128)).astype(F))
     v = O.f32_to_bf16(rng.standard_normal((2, kv_len, 128)).astype(F))
     flat = O.bf16_to_f32(O.gqa(q, k, v, kv_len))
-    rnd = O.bf16_to_f32(O.gqa(q, k, v, kv_len, flat_max=0))
+    one = O.bf16_to_f32(O.gqa(q, k, v, kv_len, split_cap=1))
     # different fp32 operation orders, the same attention to bf16 rounding
-    assert np.all(np.abs(flat - rnd) <= 2.0 ** -7 * np.abs(rnd) + 1e-4)
+    assert np.all(np.abs(flat - one) <= 2.0 ** -7 * np.abs(one) + 1e-4)
+
+
+def test_planted_missing_rescale_fails():
+    """The rescale between rounds matters: a cache whose later rounds hold
+    the dominant keys, read as one split of 10 rounds, differs from the
+    fp64 attention by far more than rounding if the earlier rounds' sums are
+    not scaled down.  Summing each round's softmax separately (what a dropped
+    rescale amounts to, restated here in fp64) fails; the oracle passes."""
+
+    rng = np.random.default_rng(12)
+    kv_len = 320
+    q32 = rng.standard_normal(2048).astype(F)
+    k32 = rng.standard_normal((2, kv_len, 128)).astype(F)
+    k32[:, 288:] += 3.0 * np.sign(q32.reshape(2, 8, 128).mean(axis=1))[:, None, :]
+    q, k = O.f32_to_bf16(q32), O.f32_to_bf16(k32)
+    v = O.f32_to_bf16(rng.standard_normal((2, kv_len, 128)).astype(F))
+    qf, kf, vf = O.bf16_to_f32(q), O.bf16_to_f32(k), O.bf16_to_f32(v)
+    want = gqa_f64(qf, kf, vf, kv_len, SCALE)
+    got = O.bf16_to_f32(O.gqa(q, k, v, kv_len, split_cap=1))
+    assert np.all(np.abs(got - want) <= 2.0 ** -7 * np.abs(want) + 2e-4)
+    s = np.einsum("gtd,ghd->ght", kf.astype(np.float64), qf.reshape(2, 8, 128).astype(np.float64)) * SCALE
+    wrong = np.zeros((2, 8, 128))
+    norm = np.zeros((2, 8, 1))
+    for r0 in range(0, kv_len, 32):
+        w = np.exp(s[:, :, r0:r0 + 32] - s[:, :, r0:r0 + 32].max(axis=2, keepdims=True))
+        wrong += np.einsum("ght,gtd->ghd", w, vf[:, r0:r0 + 32].astype(np.float64))
+        norm += w.sum(axis=2, keepdims=True)
+    assert np.abs((wrong / norm).reshape(-1) - want.reshape(-1)).max() > 0.05
 
 
 def test_planted_dropped_flat_split_fails():

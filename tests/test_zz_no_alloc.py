@@ -48,7 +48,7 @@ def test_noalloc_matches_allocating_entry_point(torch_gpu, native, stream, first
         _call(native, "kudacuda_qwen2_gqa_decode_graph_bf16_noalloc", d_q, d_k, d_v, got, capacity, d_len, stream)
         stream.synchronize()
         assert np.array_equal(host(got), host(want)), (kv_len, capacity)
-        assert np.array_equal(host(got), O.gqa(q, k, v, kv_len, chunk=O.gqa_chunk_for(capacity))), (kv_len, capacity)
+        assert np.array_equal(host(got), O.gqa(q, k, v, kv_len)), (kv_len, capacity)
 
 
 def test_noalloc_rejects_capacity_beyond_its_scratch(torch_gpu, native, stream):

@@ -19,9 +19,11 @@
 //   * weights (threads of (head, token)): the round's maximum per head, the
 //     new running maximum m', w_t = exp2(s_t - m') and the rescale
 //     exp2(m - m') of what the earlier rounds accumulated;
-//   * weighted sum: thread t owns (head t/128, dim t%128) and (head t/128 + 4,
-//     same dim): acc = acc * rescale, then acc = fma(w_t, v_t, acc) in token
-//     order; the last wave keeps the 8 sums l the same way.
+//   * weighted sum: wave w owns dims [16w, 16w+16) of all 8 heads (lane l:
+//     head l/8, dims 16w + 2(l%8) and the next, so V is read from LDS by
+//     broadcast, once per block): acc = acc * rescale, then
+//     acc = fma(w_t, v_t, acc) in token order; wave 0 keeps the 8 sums l the
+//     same way.
 // The K/V rows of the next two rounds are in flight while a round computes,
 // and the LDS is double-buffered, so a round costs two barriers.  A split of
 // one round is the plain softmax of its tokens (rescale of zero by zero).
@@ -258,10 +260,14 @@ void gqa_partial_kernel(GqaArgs a) {
     const int wh = threadIdx.x >> 5;
     const int wx = threadIdx.x & 31;
     float m_run = kNegInf;
-    // weighted sum: heads hq and hq + 4 at dim dd; the last wave also the sums l
-    const int hq = threadIdx.x / kDim;
-    const int dd = threadIdx.x % kDim;
-    const bool sums = __builtin_amdgcn_readfirstlane(wave) == kGqaWaves - 1;  // wave-uniform
+    // weighted sum: wave w owns dims [16w, 16w + 16) of all 8 heads; lane l
+    // head ph = l/8 at dims da = 16w + 2(l%8) and da + 1, so the 8 lanes of a
+    // head read each V pair by broadcast (8-byte loads, two tokens per LDS
+    // instruction) and the block reads every V element once; wave 0 also
+    // keeps the sums l (lane l: head l/8)
+    const int ph = lane >> 3;
+    const int da = 16 * wave + 2 * (lane & 7);
+    const bool sums = __builtin_amdgcn_readfirstlane(wave) == 0;  // wave-uniform
     float acc0 = 0.0f, acc1 = 0.0f, lsum = 0.0f;
 
     auto round = [&](int r, int b, uint4& kr, uint4& vr) {
@@ -313,37 +319,34 @@ void gqa_partial_kernel(GqaArgs a) {
             m_run = m_new;
         }
         __syncthreads();
-        acc0 = acc0 * s_cr[b][hq];
-        acc1 = acc1 * s_cr[b][hq + 4];
+        const float cr = s_cr[b][ph];
+        acc0 = acc0 * cr;
+        acc1 = acc1 * cr;
         if (sums) {
-            lsum = lsum * s_cr[b][lane & 7];
+            lsum = lsum * cr;
         }
-        const float* w0 = &s_wt[b][hq][0];
-        const float* w1 = &s_wt[b][hq + 4][0];
-        const float* wl = &s_wt[b][lane & 7][0];
+        const float* wp = &s_wt[b][ph][0];
         const int nq = (nv + 3) & ~3;  // whole quads: staged zeros past the end add nothing
 #pragma unroll 1
         for (int x = 0; x < nq; x += 4) {
-            const float4 c0 = *reinterpret_cast<const float4*>(w0 + x);
-            const float4 c1 = *reinterpret_cast<const float4*>(w1 + x);
-            const float e0 = s_vf[b][x + 0][dd];
-            const float e1 = s_vf[b][x + 1][dd];
-            const float e2 = s_vf[b][x + 2][dd];
-            const float e3 = s_vf[b][x + 3][dd];
-            acc0 = fmaf(c0.x, e0, acc0);
-            acc1 = fmaf(c1.x, e0, acc1);
-            acc0 = fmaf(c0.y, e1, acc0);
-            acc1 = fmaf(c1.y, e1, acc1);
-            acc0 = fmaf(c0.z, e2, acc0);
-            acc1 = fmaf(c1.z, e2, acc1);
-            acc0 = fmaf(c0.w, e3, acc0);
-            acc1 = fmaf(c1.w, e3, acc1);
+            const float4 c = *reinterpret_cast<const float4*>(wp + x);
+            const float2 e0 = *reinterpret_cast<const float2*>(&s_vf[b][x + 0][da]);
+            const float2 e1 = *reinterpret_cast<const float2*>(&s_vf[b][x + 1][da]);
+            const float2 e2 = *reinterpret_cast<const float2*>(&s_vf[b][x + 2][da]);
+            const float2 e3 = *reinterpret_cast<const float2*>(&s_vf[b][x + 3][da]);
+            acc0 = fmaf(c.x, e0.x, acc0);
+            acc1 = fmaf(c.x, e0.y, acc1);
+            acc0 = fmaf(c.y, e1.x, acc0);
+            acc1 = fmaf(c.y, e1.y, acc1);
+            acc0 = fmaf(c.z, e2.x, acc0);
+            acc1 = fmaf(c.z, e2.y, acc1);
+            acc0 = fmaf(c.w, e3.x, acc0);
+            acc1 = fmaf(c.w, e3.y, acc1);
             if (sums) {
-                const float4 cl = *reinterpret_cast<const float4*>(wl + x);
-                lsum = lsum + cl.x;
-                lsum = lsum + cl.y;
-                lsum = lsum + cl.z;
-                lsum = lsum + cl.w;
+                lsum = lsum + c.x;
+                lsum = lsum + c.y;
+                lsum = lsum + c.z;
+                lsum = lsum + c.w;
             }
         }
     };
@@ -361,49 +364,41 @@ void gqa_partial_kernel(GqaArgs a) {
     if (threadIdx.x < kHeadsPerGroup * kRound && wx == 0) {
         s_M[wh] = m_run;
     }
-    if (sums && lane < kHeadsPerGroup) {
-        s_L[lane] = lsum;
+    if (sums && (lane & 7) == 0) {
+        s_L[ph] = lsum;
     }
     __syncthreads();
-    const float av_out[2] = {acc0, acc1};
 
     float* part = a.partials;
     if (nsplit <= a.defer_max) {
         // left for the consumer kernel, which merges them by the same rule;
         // plain stores, visible to the next kernel in the stream
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            const int hl = half * 4 + hq;
-            float* dst = part + ((g * kHeadsPerGroup + hl) * a.max_splits + s) * kPartialStride;
-            dst[2 + dd] = av_out[half];
-            if (dd == 0) {
-                dst[0] = s_M[hl];
-                dst[1] = s_L[hl];
-            }
+        float* dst = part + ((g * kHeadsPerGroup + ph) * a.max_splits + s) * kPartialStride;
+        dst[2 + da] = acc0;
+        dst[3 + da] = acc1;
+        if (da == 0) {
+            dst[0] = s_M[ph];
+            dst[1] = s_L[ph];
         }
         return;
     }
     if (nsplit == 1) {
         // single split: the general merge with weight exp2(M - M) = 1
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            const int hl = half * 4 + hq;
-            const float w = exp2_fixed(s_M[hl] - s_M[hl]);
-            const float lt = fmaf(s_L[hl], w, 0.0f);
-            const float o = fmaf(av_out[half], w, 0.0f);
-            a.out[(g * kHeadsPerGroup + hl) * kDim + dd] = T::store(o / lt);
-        }
+        const float w = exp2_fixed(s_M[ph] - s_M[ph]);
+        const float lt = fmaf(s_L[ph], w, 0.0f);
+        uint16_t* out = a.out + (g * kHeadsPerGroup + ph) * kDim;
+        out[da] = T::store(fmaf(acc0, w, 0.0f) / lt);
+        out[da + 1] = T::store(fmaf(acc1, w, 0.0f) / lt);
         return;
     }
 
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-        const int hl = half * 4 + hq;
-        float* dst = part + ((g * kHeadsPerGroup + hl) * a.max_splits + s) * kPartialStride;
-        store_agent(dst + 2 + dd, av_out[half]);
-        if (dd == 0) {
-            store_agent(dst, s_M[hl]);
-            store_agent(dst + 1, s_L[hl]);
+    {
+        float* dst = part + ((g * kHeadsPerGroup + ph) * a.max_splits + s) * kPartialStride;
+        store_agent(dst + 2 + da, acc0);
+        store_agent(dst + 3 + da, acc1);
+        if (da == 0) {
+            store_agent(dst, s_M[ph]);
+            store_agent(dst + 1, s_L[ph]);
         }
     }
     if (nsplit > a.ticket_max) {
@@ -496,11 +491,7 @@ __global__ __launch_bounds__(256) void gqa_merge_kernel(GqaArgs a) {
     if (static_cast<int>(threadIdx.x) < nsplit) {
         s_l[threadIdx.x] = lsplit;
     }
-    float mloc = mine;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        mloc = fmaxf(mloc, __shfl_xor(mloc, o, 64));
-    }
+    const float mloc = span_max<64>(mine);
     if ((threadIdx.x & 63) == 0) {
         s_red[threadIdx.x >> 6] = mloc;
     }
@@ -510,18 +501,25 @@ __global__ __launch_bounds__(256) void gqa_merge_kernel(GqaArgs a) {
         s_w[threadIdx.x] = exp2_fixed(mine - M);
     }
     __syncthreads();
+    // LDS entries past nsplit (and past ngroups) are read but not used:
+    // the loads stay unconditional and in flight together
     const int ngroups = (nsplit + kGqaMergeGroup - 1) / kGqaMergeGroup;
     if (row < ngroups) {
         const int x0 = row * kGqaMergeGroup;
+        float vx[kGqaMergeGroup], wx[kGqaMergeGroup], lx[kGqaMergeGroup];
+#pragma unroll
+        for (int i = 0; i < kGqaMergeGroup; ++i) {
+            vx[i] = s_v[x0 + i][d];
+            wx[i] = s_w[x0 + i];
+            lx[i] = s_l[x0 + i];
+        }
         float og = 0.0f;
         float lg = 0.0f;
 #pragma unroll
         for (int i = 0; i < kGqaMergeGroup; ++i) {
-            const int x = x0 + i;
-            if (x < nsplit) {
-                og = fmaf(s_v[x][d], s_w[x], og);
-                lg = fmaf(s_l[x], s_w[x], lg);
-            }
+            const bool live = x0 + i < nsplit;
+            og = live ? fmaf(vx[i], wx[i], og) : og;
+            lg = live ? fmaf(lx[i], wx[i], lg) : lg;
         }
         s_go[row][d] = og;
         if (d == 0) {
@@ -530,11 +528,18 @@ __global__ __launch_bounds__(256) void gqa_merge_kernel(GqaArgs a) {
     }
     __syncthreads();
     if (threadIdx.x < kSlice) {
-        float o = s_go[0][d];
-        float lt = s_gl[0];
-        for (int j = 1; j < ngroups; ++j) {
-            o = o + s_go[j][d];
-            lt = lt + s_gl[j];
+        float go[kMergeGroups], gl[kMergeGroups];
+#pragma unroll
+        for (int j = 0; j < kMergeGroups; ++j) {
+            go[j] = s_go[j][d];
+            gl[j] = s_gl[j];
+        }
+        float o = go[0];
+        float lt = gl[0];
+#pragma unroll
+        for (int j = 1; j < kMergeGroups; ++j) {
+            o = j < ngroups ? o + go[j] : o;
+            lt = j < ngroups ? lt + gl[j] : lt;
         }
         a.out[static_cast<int64_t>(h) * kDim + d0 + d] = T::store(o / lt);
     }

@@ -187,6 +187,11 @@ __device__ __forceinline__ void store_agent(float* p, float v) {
 __device__ __forceinline__ void store_agent(uint32_t* p, uint32_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// two adjacent floats (8-byte aligned) as one 8-byte agent-scope store
+__device__ __forceinline__ void store_agent_pair(float* p, float lo, float hi) {
+    const uint64_t v = static_cast<uint64_t>(__float_as_uint(lo)) | (static_cast<uint64_t>(__float_as_uint(hi)) << 32);
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ float load_agent(const float* p) {
     return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

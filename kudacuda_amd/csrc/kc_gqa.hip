@@ -225,8 +225,14 @@ void gqa_partial_kernel(GqaArgs a) {
     // waves' memory counters see the same sequence every round and each round
     // waits only for its own rows.
     uint4 k0, v0, k1, v1;
-    load_row(kbase, vbase, s * c_guess + gi, a.capacity, k0, v0);
-    load_row(kbase, vbase, s * c_guess + kRound + gi, a.capacity, k1, v1);
+    {
+        // the guessed split's own rows only (a one-round split re-reads its
+        // last row instead of the next split's first round)
+        const int64_t g0 = s * c_guess;
+        const int64_t g_end = g0 + c_guess < a.capacity ? g0 + c_guess : a.capacity;
+        load_row(kbase, vbase, g0 + gi, g_end, k0, v0);
+        load_row(kbase, vbase, g0 + kRound + gi, g_end, k1, v1);
+    }
 
     const int64_t L = read_kv_len(a);
     const int64_t C = gqa_split_tokens(L, a.split_cap);
@@ -374,11 +380,9 @@ void gqa_partial_kernel(GqaArgs a) {
         // left for the consumer kernel, which merges them by the same rule;
         // plain stores, visible to the next kernel in the stream
         float* dst = part + ((g * kHeadsPerGroup + ph) * a.max_splits + s) * kPartialStride;
-        dst[2 + da] = acc0;
-        dst[3 + da] = acc1;
+        *reinterpret_cast<float2*>(dst + 2 + da) = make_float2(acc0, acc1);
         if (da == 0) {
-            dst[0] = s_M[ph];
-            dst[1] = s_L[ph];
+            *reinterpret_cast<float2*>(dst) = make_float2(s_M[ph], s_L[ph]);
         }
         return;
     }
@@ -386,19 +390,18 @@ void gqa_partial_kernel(GqaArgs a) {
         // single split: the general merge with weight exp2(M - M) = 1
         const float w = exp2_fixed(s_M[ph] - s_M[ph]);
         const float lt = fmaf(s_L[ph], w, 0.0f);
-        uint16_t* out = a.out + (g * kHeadsPerGroup + ph) * kDim;
-        out[da] = T::store(fmaf(acc0, w, 0.0f) / lt);
-        out[da + 1] = T::store(fmaf(acc1, w, 0.0f) / lt);
+        const uint32_t lo = T::store(fmaf(acc0, w, 0.0f) / lt);
+        const uint32_t hi = T::store(fmaf(acc1, w, 0.0f) / lt);
+        *reinterpret_cast<uint32_t*>(a.out + (g * kHeadsPerGroup + ph) * kDim + da) = lo | (hi << 16);
         return;
     }
 
     {
+        // 8-byte pairs (the row's floats 2 + da, 3 + da and 0, 1 are 8-byte aligned)
         float* dst = part + ((g * kHeadsPerGroup + ph) * a.max_splits + s) * kPartialStride;
-        store_agent(dst + 2 + da, acc0);
-        store_agent(dst + 3 + da, acc1);
+        store_agent_pair(dst + 2 + da, acc0, acc1);
         if (da == 0) {
-            store_agent(dst, s_M[ph]);
-            store_agent(dst + 1, s_L[ph]);
+            store_agent_pair(dst, s_M[ph], s_L[ph]);
         }
     }
     if (nsplit > a.ticket_max) {

@@ -175,10 +175,10 @@ class Bench:
             del ws
             self.torch.cuda.empty_cache()
 
-    def gqa(self) -> None:
+    def gqa(self, lengths: tuple[int, ...] = GQA_LENGTHS) -> None:
         s = self.stream.cuda_stream
         scale = 1.0 / math.sqrt(128.0)
-        for length in GQA_LENGTHS:
+        for length in lengths:
             nbytes = 1024 * length + 8192
             n = self.copies_for(nbytes)
             caches = [(self.rand_bf16(2 * length * 128), self.rand_bf16(2 * length * 128)) for _ in range(n)]
@@ -215,6 +215,8 @@ def main(argv: list[str] | None = None) -> int:
     parser.add_argument("--launches", type=int, default=256)
     parser.add_argument("--copy-mib", type=int, default=0,
                         help="first run 3 plain device copies of this many MiB (counter calibration)")
+    parser.add_argument("--gqa-lengths", type=int, nargs="+", default=list(GQA_LENGTHS),
+                        help="kv lengths of config 4")
     args = parser.parse_args(argv)
     import torch
 
@@ -231,7 +233,10 @@ def main(argv: list[str] | None = None) -> int:
                   flush=True)
             del src, dst
         for config in args.configs:
-            {1: bench.gemv, 2: bench.qkv, 3: bench.mlp, 4: bench.gqa, 6: bench.prefill_gemm}[config]()
+            if config == 4:
+                bench.gqa(tuple(args.gqa_lengths))
+            else:
+                {1: bench.gemv, 2: bench.qkv, 3: bench.mlp, 6: bench.prefill_gemm}[config]()
     bench.native.close()
     return 0
 

@@ -63,6 +63,28 @@ def measured_traffic(kernel: str) -> int | None:
     return None if entry is None else int(entry["hbm_bytes"])
 
 
+# per-config case -> the kernels of profiles/traffic.json one launch runs
+CONFIG_TRAFFIC = {
+    ("nf4_gemv_2048x2048", 0): ("gemv",),
+    ("fused_rmsnorm_qkv_nf4", 0): ("qkv",),
+    ("swiglu_nf4_gate_up", 0): ("gate_up",),
+    ("mlp_nf4_gate_up_down", 0): ("gate_up", "down"),
+    ("gqa_decode_bf16", 8192): ("gqa_partial_8192", "gqa_merge_8192"),
+    ("gqa_decode_bf16", 32768): ("gqa_partial_32768", "gqa_merge_32768"),
+}
+
+
+def config_traffic(case: dict) -> int | None:
+    """Measured HBM bytes per launch of a per-config case (sum over its
+    kernels), or None where no PMC run covers it."""
+
+    kernels = CONFIG_TRAFFIC.get((case["op"], case.get("kv_len", 0)))
+    if kernels is None:
+        return None
+    parts = [measured_traffic(k) for k in kernels]
+    return None if any(x is None for x in parts) else sum(parts)
+
+
 def op_bytes(cfg, vocab: int, kv_len: int) -> dict[str, int]:
     """Algorithmic HBM bytes per launch of each kernel of the decode step:
     NF4 codes + fp32 absmax + bf16 vectors read and written once."""
@@ -376,7 +398,7 @@ def main(argv: list[str] | None = None) -> int:
                 entry["kv_len"] = case["kv_len"]
             entry.update(us=case["us"], bytes=case["bytes"],
                          roofline={"bound": "hbm", "achieved": case["gbs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                                   "frac": case["frac"]})
+                                   "frac": case["frac"], "traffic": config_traffic(case)})
             cpu = cpu_cases.get((case["op"], case.get("kv_len", 0)))
             entry["cpu_baseline"] = cpu
             if cpu is not None:

@@ -66,8 +66,8 @@ constexpr int kDim = 128;
 constexpr int kPartialStride = kGqaPartialStride;
 static_assert(kPartialStride == 2 + kDim, "partial layout: max, sum, acc[128]");
 constexpr int kInKernelSplits = 32;
-constexpr int kMergeMaxSplits = kGqaSplitCap;  // every plan's split count: split_limit only lowers it
-static_assert(kMergeMaxSplits <= 256, "the merge kernel loads one split's max and sum per thread");
+constexpr int kMergeMaxSplits = 256;  // one split's max and sum per merge thread
+static_assert(kGqaSplitCap <= kMergeMaxSplits, "every plan's split count (split_limit only lowers it)");
 constexpr int kMergeDims = 16;              // dims per merge block
 constexpr int kMergeGroups = kMergeMaxSplits / kGqaMergeGroup;
 constexpr int kPitch = kRound + 4;          // score / weight rows: the 8 heads on distinct banks

@@ -470,6 +470,10 @@ KCO_API void kco_gqa(int act, const uint16_t* q, const uint16_t* kc, const uint1
                         float a = acc[hl][d] * r;
                         for (int t = 0; t < nv; ++t)
                             a = fmaf(w[t], act_load(act, vc[((int64_t)g * capacity + base + t) * 128 + d]), a);
+                        /* the kernel's sum runs over whole quads of tokens, the
+                         * slots past the end holding weight 0 and value 0: a
+                         * zero product added (turns -0 into +0, else exact) */
+                        if (nv & 3) a = fmaf(0.0f, 0.0f, a);
                         acc[hl][d] = a;
                     }
                     m[hl] = mn;

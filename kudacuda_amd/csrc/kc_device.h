@@ -175,12 +175,25 @@ __device__ __forceinline__ float2 wave_sum2(float a, float b) {
 
 // -------------------------------------------------- cross-block exchange
 // Blocks of one launch that hand results to a "last block" (ticket pattern)
-// exchange only a few words.  A device-scope fence would write back and
-// invalidate the whole L2 of the XCD (the XCDs' L2 caches are not coherent
-// with each other), which costs microseconds per block.  Instead the
-// exchanged words are written and read with agent-scope atomic stores/loads,
-// which are coherent across XCDs, and every wave waits for its own stores to
-// complete before the block increments the ticket.
+// exchange only a few words.  The hand-over, and what each step compiles to
+// on gfx950 (checked in this build's assembly):
+//   1. each thread writes its words with agent-scope atomic stores
+//      (global_store_* ... sc1: written through the XCD's L2, which is not
+//      coherent with the other XCDs' L2 caches);
+//   2. every wave waits for its own stores (s_waitcnt vmcnt(0)), then the
+//      block barrier;
+//   3. one thread takes the ticket with an agent-scope acquire-release
+//      fetch-add (buffer_wbl2 sc1, global_atomic_add, buffer_inv sc1): the
+//      release orders the block's stores before the increment under the HIP
+//      memory model, the acquire orders the other blocks' stores before this
+//      block's reads;
+//   4. the last block reads the words with agent-scope atomic loads
+//      (global_load_* ... sc1).
+// Steps 1, 2 and 4 alone carry the data on this hardware; step 3's fences
+// make the hand-over correct by the memory model instead of by those cache
+// bits, for ~0.2 us per launch of a few publishing blocks (each release's L2
+// write-back costs ~0.3 us and those of one XCD serialise, so a launch with
+// hundreds of publishing blocks keeps a relaxed ticket: lm_head).
 __device__ __forceinline__ void store_agent(float* p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -194,6 +207,10 @@ __device__ __forceinline__ void store_agent_pair(float* p, float lo, float hi) {
 }
 __device__ __forceinline__ float load_agent(const float* p) {
     return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// The ticket of step 3: returns the counter's value before the increment.
+__device__ __forceinline__ uint32_t take_ticket(uint32_t* counter) {
+    return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
 }
 // Wait until this wave's vector memory operations (the exchange stores) have
 // completed; call before the barrier that precedes the ticket increment.

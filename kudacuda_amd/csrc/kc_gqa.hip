@@ -35,7 +35,7 @@
 //   * one split: finished in place, out = acc*1 / (sum*1), the general merge
 //     with weight exp2(0) = 1;
 //   * up to ticket_max (<= kInKernelSplits): merged by the last block of the
-//     KV head to finish (a ticket of agent-scope atomics, reset by that block,
+//     KV head to finish (an agent-scope acquire-release ticket, reset by that block,
 //     so the launch is capture-safe);
 //   * more: merged by gqa_merge_kernel (grid: query head x 16-dim slice),
 //     launched after the partial kernel whenever the grid allows more than
@@ -409,11 +409,12 @@ void gqa_partial_kernel(GqaArgs a) {
     }
 
     // ---- ticket: the last block of this KV head merges all splits (the
-    // partials travel through agent-scope atomic stores/loads, no fences)
+    // partials travel through agent-scope atomic stores/loads and the
+    // acquire-release ticket)
     wait_own_stores();
     __syncthreads();
     if (threadIdx.x == 0) {
-        const uint32_t prev = atomicAdd(a.counters + g, 1u);
+        const uint32_t prev = take_ticket(a.counters + g);
         s_last = prev == static_cast<uint32_t>(nsplit - 1) ? 1 : 0;
     }
     __syncthreads();

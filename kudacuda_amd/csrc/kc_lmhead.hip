@@ -188,7 +188,12 @@ __global__ __launch_bounds__(kLmThreads) void lm_head_kernel(LmHeadArgs a) {
         }
     }
 
-    // block winners travel through agent-scope atomic stores/loads (no fences)
+    // block winners travel through agent-scope atomic stores (written through
+    // the L2) that every wave waits for, and agent-scope loads (which miss
+    // the non-coherent caches); the ticket is a relaxed fetch-add.  768
+    // publishing blocks make take_ticket's release too dear here: its L2
+    // write-back (buffer_wbl2 sc1) costs ~0.3 us and the blocks of an XCD
+    // serialise on it, 107 -> 135 us per token.
     wait_own_stores();
     __syncthreads();
     if (threadIdx.x == 0) {

@@ -21,6 +21,8 @@
 // (kernels/common/nf4_tiled_gemv.cuh:61-168: norm in fp32, dot in fp32,
 // bias added in fp32 before the single output rounding) and its SwiGLU
 // (kernels/common/nf4_swiglu_bf16.cuh:61-164: silu(g) * u in fp32).
+#include <utility>
+
 #include "kc_device.h"
 #include "kc_kernels.h"
 
@@ -92,6 +94,12 @@ __device__ __forceinline__ RowPair map_task(const Nf4RowsArgs& a, int64_t task) 
 __device__ __forceinline__ void fetch_row(const Nf4RowsArgs& a, int m, int64_t r, int lane, uint4& pk, float& am) {
     pk = reinterpret_cast<const uint4*>(a.w[m] + r * 1024)[lane];
     am = a.absmax[m][r * 32 + (lane >> 1)];
+}
+
+// wx[x] = lane x's value of every lane's 16-lane row, for x in X
+template <int... X>
+__device__ __forceinline__ void row_bcast_all(float v, float* wx, std::integer_sequence<int, X...>) {
+    ((wx[X] = row_bcast<X>(v)), ...);
 }
 
 // Small per-task operands of the epilogue (bias, residual, rotary
@@ -319,15 +327,8 @@ __global__ __launch_bounds__(NTH) void nf4_rows2048_kernel(Nf4RowsArgs a, int64_
             }
             const float wi = exp2_fixed(mi - M);
             float wx[kGqaMaxDefer];
-            wx[0] = row_bcast<0>(wi);
-            wx[1] = row_bcast<1>(wi);
-            wx[2] = row_bcast<2>(wi);
-            wx[3] = row_bcast<3>(wi);
-            wx[4] = row_bcast<4>(wi);
-            wx[5] = row_bcast<5>(wi);
-            wx[6] = row_bcast<6>(wi);
-            wx[7] = row_bcast<7>(wi);
-            static_assert(kGqaMaxDefer == 8, "one broadcast per deferred split");
+            static_assert(kGqaMaxDefer <= 16, "one broadcast per deferred split, within a 16-lane row");
+            row_bcast_all(wi, wx, std::make_integer_sequence<int, kGqaMaxDefer>{});
             float lt = 0.0f;
             float o[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll

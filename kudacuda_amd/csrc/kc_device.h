@@ -238,20 +238,41 @@ __device__ __forceinline__ uint32_t byte_shl3(uint32_t x) {
     return r;
 }
 
+// Where a lane finds byte value e's entry of the pair table in LDS: the
+// block's single copy (offset e * 8, one byte-select shift) ...
+struct PairLookup {
+    const char* base;
+    template <int B>
+    __device__ __forceinline__ const float2* entry(uint32_t w) const {
+        return reinterpret_cast<const float2*>(base + byte_shl3<B>(w));
+    }
+};
+// ... or the lane-sliced copy (see nf4_fill_sliced): offset e * 256 + 8 s for
+// the lane's slot s = lane % 32, formed by one byte permute from the code
+// word and the lane's 8 s (bytes, low to high: 8 s, byte B of w, 0, 0).
+struct SlicedLookup {
+    const char* base;
+    uint32_t slot8;
+    template <int B>
+    __device__ __forceinline__ const float2* entry(uint32_t w) const {
+        return reinterpret_cast<const float2*>(base + __builtin_amdgcn_perm(w, slot8, 0x0c0c0400u | (B << 8)));
+    }
+};
+
 // Codebook values of the 32 codes of one chunk, gathered from the LDS pair
 // table before any arithmetic so the lookups overlap.  Entry e of the table
 // holds (code[e >> 4], code[e & 15]), the values of both nibbles of byte e
-// (even element in the high nibble), so each byte costs one byte-select
-// shift (its offset e * 8) and one 8-byte LDS read.
-__device__ __forceinline__ void nf4_gather32(const uint4 pk, const float* pairs, float* cw) {
+// (even element in the high nibble), so each byte costs one offset
+// instruction and one 8-byte LDS read.
+template <typename Lookup>
+__device__ __forceinline__ void nf4_gather32(const uint4 pk, const Lookup& lut, float* cw) {
     const uint32_t w[4] = {pk.x, pk.y, pk.z, pk.w};
-    const char* base = reinterpret_cast<const char*>(pairs);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const float2 p0 = *reinterpret_cast<const float2*>(base + byte_shl3<0>(w[i]));
-        const float2 p1 = *reinterpret_cast<const float2*>(base + byte_shl3<1>(w[i]));
-        const float2 p2 = *reinterpret_cast<const float2*>(base + byte_shl3<2>(w[i]));
-        const float2 p3 = *reinterpret_cast<const float2*>(base + byte_shl3<3>(w[i]));
+        const float2 p0 = *lut.template entry<0>(w[i]);
+        const float2 p1 = *lut.template entry<1>(w[i]);
+        const float2 p2 = *lut.template entry<2>(w[i]);
+        const float2 p3 = *lut.template entry<3>(w[i]);
         cw[8 * i + 0] = p0.x;
         cw[8 * i + 1] = p0.y;
         cw[8 * i + 2] = p1.x;
@@ -264,10 +285,11 @@ __device__ __forceinline__ void nf4_gather32(const uint4 pk, const float* pairs,
 }
 
 // Dot of one 32-element chunk with x[0..31] (already in fp32), before the
-// absmax multiply.  pairs points at the LDS copy of the pair table.
-__device__ __forceinline__ float nf4_chunk_dot_raw(const uint4 pk, const float* x, const float* pairs) {
+// absmax multiply, with the pair table in LDS at `lut`.
+template <typename Lookup>
+__device__ __forceinline__ float nf4_chunk_dot(const uint4 pk, const float* x, const Lookup& lut) {
     float cw[32];
-    nf4_gather32(pk, pairs, cw);
+    nf4_gather32(pk, lut, cw);
     float a[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -279,6 +301,10 @@ __device__ __forceinline__ float nf4_chunk_dot_raw(const uint4 pk, const float* 
         a[i] = acc;
     }
     return (a[0] + a[1]) + (a[2] + a[3]);
+}
+// ... with the block's single copy of the table at `pairs`.
+__device__ __forceinline__ float nf4_chunk_dot_raw(const uint4 pk, const float* x, const float* pairs) {
+    return nf4_chunk_dot(pk, x, PairLookup{reinterpret_cast<const char*>(pairs)});
 }
 
 // Sum of squares of 32 consecutive elements, same accumulator split as a
@@ -363,6 +389,30 @@ __device__ __forceinline__ void pair_entry_store(float* pairs, float2 e) {
     if (threadIdx.x < kNf4PairEntries) {
         reinterpret_cast<float2*>(pairs)[threadIdx.x] = e;
     }
+}
+
+// Lane-sliced copy of the pair table for kernels with few, large blocks: 32
+// copies interleaved so that slot s of entry e sits at byte e * 256 + 8 s.
+// Lane l reads slot l % 32, so its lookups always fall in bank pair
+// (l % 32) % 16 and the 16 lanes an LDS pass serves for 8-byte reads never
+// share a bank; random entries of the single table collide (about two
+// thirds of its LDS cycles were bank-conflict stalls).  64 KiB.
+constexpr int kNf4Slots = 32;
+constexpr int kNf4SlicedFloats = 2 * kNf4PairEntries * kNf4Slots;
+// Thread t < 256 writes its entry (pair_entry_fetch) into all 32 slots, slot
+// (j + t) % 32 at step j, so the 16 lanes of a pass write 16 bank pairs.
+// The caller publishes the table with a block barrier.
+__device__ __forceinline__ void sliced_entry_store(float* sliced, float2 e) {
+    if (threadIdx.x < kNf4PairEntries) {
+        float2* row = reinterpret_cast<float2*>(sliced) + threadIdx.x * kNf4Slots;
+#pragma unroll 8
+        for (int j = 0; j < kNf4Slots; ++j) {
+            row[(j + threadIdx.x) & (kNf4Slots - 1)] = e;
+        }
+    }
+}
+__device__ __forceinline__ SlicedLookup sliced_lookup(const float* sliced) {
+    return SlicedLookup{reinterpret_cast<const char*>(sliced), (threadIdx.x & (kNf4Slots - 1)) * 8u};
 }
 
 }  // namespace kc

@@ -205,7 +205,10 @@ __global__ __launch_bounds__(NTH) void nf4_rows2048_kernel(Nf4RowsArgs a, int64_
     constexpr bool kCoop = MODE != RowMode::kGemv;
     static_assert(!kCoop || (NTH >= 256 && NTH % 64 == 0), "waves 0..3 compute the shared norm");
     static_assert(!ATTN || NTH == kRowsThreads, "merge layout");
-    __shared__ __attribute__((aligned(16))) float cb[2 * kNf4PairEntries];
+    // gate/up (one large block per CU) reads the lane-sliced table, the other
+    // modes (many small blocks per CU) the single one
+    constexpr bool kSliced = MODE == RowMode::kSwiGlu;
+    __shared__ __attribute__((aligned(16))) float cb[kSliced ? kNf4SlicedFloats : 2 * kNf4PairEntries];
     __shared__ __attribute__((aligned(16))) uint16_t s_xa[ATTN ? 2048 : 8];
     __shared__ float s_ss[4];
     __shared__ __attribute__((aligned(16))) float s_xn[kCoop ? 64 * kNormPitch : 4];
@@ -371,7 +374,11 @@ __global__ __launch_bounds__(NTH) void nf4_rows2048_kernel(Nf4RowsArgs a, int64_
             s_ss[wave] = acc;
         }
     }
-    pair_entry_store(cb, pair_entry);
+    if constexpr (kSliced) {
+        sliced_entry_store(cb, pair_entry);
+    } else {
+        pair_entry_store(cb, pair_entry);
+    }
     __syncthreads();
     if constexpr (ATTN) {
         if (merged) {
@@ -449,13 +456,19 @@ __global__ __launch_bounds__(NTH) void nf4_rows2048_kernel(Nf4RowsArgs a, int64_
             __builtin_amdgcn_sched_barrier(0);
         }
         float d0, d1 = 0.0f;
+        auto dot = [&](const uint4& w) {
+            if constexpr (kSliced) {
+                return nf4_chunk_dot(w, xn, sliced_lookup(cb));
+            } else {
+                return nf4_chunk_dot_raw(w, xn, cb);
+            }
+        };
         if (tasks[i].has1) {
-            const float2 d = wave_sum2(nf4_chunk_dot_raw(pk[i][0], xn, cb) * am[i][0],
-                                       nf4_chunk_dot_raw(pk[i][1], xn, cb) * am[i][1]);
+            const float2 d = wave_sum2(dot(pk[i][0]) * am[i][0], dot(pk[i][1]) * am[i][1]);
             d0 = d.x;
             d1 = d.y;
         } else {
-            d0 = wave_sum(nf4_chunk_dot_raw(pk[i][0], xn, cb) * am[i][0]);
+            d0 = wave_sum(dot(pk[i][0]) * am[i][0]);
         }
         if constexpr (MODE == RowMode::kSwiGlu) {
             gate = lane == i ? d0 : gate;

@@ -393,18 +393,24 @@ __device__ __forceinline__ void pair_entry_store(float* pairs, float2 e) {
 
 // Lane-sliced copy of the pair table for kernels with few, large blocks: 32
 // copies interleaved so that slot s of entry e sits at byte e * 256 + 8 s.
-// Lane l reads slot l % 32, so its lookups always fall in bank pair
-// (l % 32) % 16 and the 16 lanes an LDS pass serves for 8-byte reads never
-// share a bank; random entries of the single table collide (about two
-// thirds of its LDS cycles were bank-conflict stalls).  64 KiB.
+// Lane l reads slot l % 32, so its lookups always fall in bank pair l % 32,
+// and the 32 lanes an LDS pass serves for 8-byte reads (64 banks of 4 bytes)
+// never share a bank; random entries of the single table collide (about two
+// thirds of its LDS cycles were bank-conflict stalls).  Fewer slots (16 or
+// 8, half or a quarter of the fill) put two or four lanes of a pass on one
+// bank pair and measured slower.  64 KiB; the entry stride (kNf4SlotStride
+// slots, 256 bytes) is what one byte permute can form, kNf4Slots of its
+// slots are filled and read.
+constexpr int kNf4SlotStride = 32;
 constexpr int kNf4Slots = 32;
-constexpr int kNf4SlicedFloats = 2 * kNf4PairEntries * kNf4Slots;
-// Thread t < 256 writes its entry (pair_entry_fetch) into all 32 slots, slot
-// (j + t) % 32 at step j, so the 16 lanes of a pass write 16 bank pairs.
-// The caller publishes the table with a block barrier.
+static_assert(kNf4Slots <= kNf4SlotStride && (kNf4Slots & (kNf4Slots - 1)) == 0, "slots tile the stride");
+constexpr int kNf4SlicedFloats = 2 * kNf4PairEntries * kNf4SlotStride;
+// Thread t < 256 writes its entry (pair_entry_fetch) into every slot, slot
+// (j + t) % kNf4Slots at step j, so the 32 lanes of a pass write 32 bank
+// pairs.  The caller publishes the table with a block barrier.
 __device__ __forceinline__ void sliced_entry_store(float* sliced, float2 e) {
     if (threadIdx.x < kNf4PairEntries) {
-        float2* row = reinterpret_cast<float2*>(sliced) + threadIdx.x * kNf4Slots;
+        float2* row = reinterpret_cast<float2*>(sliced) + threadIdx.x * kNf4SlotStride;
 #pragma unroll 8
         for (int j = 0; j < kNf4Slots; ++j) {
             row[(j + threadIdx.x) & (kNf4Slots - 1)] = e;

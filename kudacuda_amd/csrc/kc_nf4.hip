@@ -516,7 +516,8 @@ __global__ __launch_bounds__(NTH) void nf4_rows2048_kernel(Nf4RowsArgs a, int64_
 template <typename T, int NCHUNK, int R>
 __global__ __launch_bounds__(64 * ((NCHUNK + 63) / 64)) void nf4_down_kernel(Nf4DownArgs a) {
     constexpr int W = (NCHUNK + 63) / 64;
-    __shared__ __attribute__((aligned(16))) float cb[2 * kNf4PairEntries];
+    // the pair table and one spare entry that threads past the table overwrite
+    __shared__ __attribute__((aligned(16))) float cb[2 * kNf4PairEntries + 2];
     __shared__ float red[R][W];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -536,9 +537,13 @@ __global__ __launch_bounds__(64 * ((NCHUNK + 63) / 64)) void nf4_down_kernel(Nf4
     for (int i = 0; i < 4; ++i) {
         xr[i] = src[i];
     }
-    // thread t < R finishes row rbase + t
+    // thread t < R finishes row rbase + t.  The residual load is unconditional
+    // (from x when there is none): a load under a branch makes the compiler
+    // wait for every load issued before it, so the rows would be requested
+    // only after the activation chunk had arrived.
     const int64_t my_row = rbase + (threadIdx.x % R) < last_row ? rbase + (threadIdx.x % R) : last_row;
-    const uint16_t res = a.residual != nullptr ? a.residual[my_row] : static_cast<uint16_t>(0);
+    const bool has_res = a.residual != nullptr;
+    const uint16_t res = *(has_res ? a.residual + my_row : a.x);
 
     uint4 pk[R];
     float am[R];
@@ -552,7 +557,11 @@ __global__ __launch_bounds__(64 * ((NCHUNK + 63) / 64)) void nf4_down_kernel(Nf4
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    pair_entry_store(cb, pair_entry);
+    // Every thread stores (those past the table into the spare entry): a
+    // store under a branch lets the compiler sink the entry's load behind the
+    // rows and wait for all of them before the barrier.
+    reinterpret_cast<float2*>(cb)[threadIdx.x < kNf4PairEntries ? threadIdx.x : kNf4PairEntries] = pair_entry;
+    __builtin_amdgcn_sched_barrier(0);  // nothing that waits for a row before the barrier
     __syncthreads();
     float xv[32];
 #pragma unroll
@@ -579,7 +588,7 @@ __global__ __launch_bounds__(64 * ((NCHUNK + 63) / 64)) void nf4_down_kernel(Nf4
         for (int w = 1; w < W; ++w) {
             s = s + red[threadIdx.x][w];
         }
-        if (a.residual != nullptr) {
+        if (has_res) {
             s = T::load(res) + T::load(T::store(s));
         }
         a.out[r] = T::store(s);

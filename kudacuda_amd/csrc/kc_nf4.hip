@@ -742,6 +742,9 @@ hipError_t launch_nf4_down11008(Act act, const Nf4DownArgs& a, hipStream_t strea
     if (a.rows <= 0) {
         return hipSuccess;
     }
+    if (a.x == nullptr || a.w == nullptr || a.absmax == nullptr || a.out == nullptr) {
+        return hipErrorInvalidValue;  // the kernel also reads x in place of an absent residual
+    }
     const int64_t blocks = (a.rows + kRows - 1) / kRows;
     if (act == Act::kBf16) {
         hipLaunchKernelGGL((nf4_down_kernel<Bf16, kChunks, kRows>), dim3(static_cast<unsigned>(blocks)),

@@ -112,6 +112,9 @@ struct Handle {
     int32_t* argmax_slot = nullptr;
     // this device's copy of the file-scope `scratch` array (device address)
     unsigned char* static_scratch = nullptr;
+    // stream of the last call that used the handle's scratch (claim_scratch)
+    hipStream_t scratch_stream = nullptr;
+    bool scratch_used = false;
 };
 
 Handle* as_handle(void* raw) { return reinterpret_cast<Handle*>(raw); }
@@ -132,6 +135,35 @@ bool ready(Handle* h, const char* symbol) {
         h->set_error(std::string(symbol) + " called before kudacuda_freeze");
         return false;
     }
+    return true;
+}
+
+// Calls that use the handle's scratch (split partials, ticket counters,
+// argmax winners, GEMM partials) must not overlap on the GPU.  A call on
+// another stream than the previous scratch user is refused while that stream
+// still has work queued, which may still be using the scratch; a call on the
+// same stream is ordered after it.  Launches into a stream capture are not
+// checked: they run when the graph is replayed (graphs are one per handle).
+bool claim_scratch(Handle* h, const char* symbol, hipStream_t s) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
+        return true;
+    }
+    if (h->scratch_used && s != h->scratch_stream) {
+        hipStreamCaptureStatus ps = hipStreamCaptureStatusNone;
+        const bool prev_capturing =
+            hipStreamIsCapturing(h->scratch_stream, &ps) == hipSuccess && ps != hipStreamCaptureStatusNone;
+        const hipError_t q = prev_capturing ? hipSuccess : hipStreamQuery(h->scratch_stream);
+        (void)hipGetLastError();  // a busy (or since destroyed) stream is an answer, not an error
+        if (q == hipErrorNotReady) {
+            h->set_error(std::string(symbol) +
+                         ": the handle's scratch is in use by work still queued on another stream; "
+                         "synchronise that stream first or use one handle per stream");
+            return false;
+        }
+    }
+    h->scratch_stream = s;
+    h->scratch_used = true;
     return true;
 }
 
@@ -302,6 +334,9 @@ int gqa_direct(void* raw, const char* symbol, Act act, uint64_t q, uint64_t k, u
     a.kv_len_host = kv_len;
     set_gqa_plan(a, kv_len, 0);
     a.qk_scale_log2 = s.scale * kLog2e;
+    if (!claim_scratch(h, symbol, as_stream(stream))) {
+        return 1;
+    }
     return finish(h, symbol, launch_gqa_decode(act, a, as_stream(stream)));
 }
 
@@ -344,6 +379,9 @@ int gqa_graph(void* raw, const char* symbol, Act act, uint64_t q, uint64_t k, ui
     } else {
         a.partials = h->gqa_partials;
         a.counters = h->counters;
+        if (!claim_scratch(h, symbol, as_stream(stream))) {
+            return 1;
+        }
     }
     a.qk_scale_log2 = s.scale * kLog2e;
     return finish(h, symbol, launch_gqa_decode(act, a, as_stream(stream)));
@@ -685,6 +723,7 @@ using kc::finish;
 using kc::Handle;
 using kc::ptr;
 using kc::ready;
+using kc::claim_scratch;
 
 extern "C" {
 
@@ -1051,6 +1090,9 @@ int kudacuda_nf4_gemm_bf16(void* raw, uint64_t input, uint64_t weight_packed, ui
     a.partials = h->gemm_partials;
     a.partial_floats = kc::kGemmScratchFloats;
     const kc::GemmEpi epi = residual != 0 ? kc::GemmEpi::kResidual : kc::GemmEpi::kBias;
+    if (!claim_scratch(h, symbol, as_stream(stream))) {
+        return 1;
+    }
     return finish(h, symbol, kc::gemm_chunks(epi, a, tokens, as_stream(stream)));
 }
 
@@ -1081,6 +1123,9 @@ int kudacuda_nf4_gemm_swiglu_bf16(void* raw, uint64_t input, uint64_t gate_weigh
     a.k = in_features;
     a.partials = h->gemm_partials;
     a.partial_floats = kc::kGemmScratchFloats;
+    if (!claim_scratch(h, symbol, as_stream(stream))) {
+        return 1;
+    }
     return finish(h, symbol, kc::gemm_chunks(kc::GemmEpi::kSwiGlu, a, tokens, as_stream(stream)));
 }
 
@@ -1160,6 +1205,9 @@ int kudacuda_qwen2_gqa_decode_workspace_v3(void* raw, uint64_t query, uint64_t k
     // the caller's workspace holds 16 x 8 x 130 floats (reference contract)
     kc::set_gqa_plan(a, kv_capacity, 8);
     a.qk_scale_log2 = scale * kc::kLog2e;
+    if (!claim_scratch(h, symbol, as_stream(stream))) {
+        return 1;
+    }
     return finish(h, symbol, kc::launch_gqa_decode(Act::kF16, a, as_stream(stream)));
 }
 
@@ -1253,6 +1301,9 @@ int kudacuda_lm_head_argmax_bf16(void* raw, uint64_t input, uint64_t norm_weight
     a.block_best = h->lm_best;
     a.counter = h->counters + 2;
     a.argmax_out = ptr<int32_t>(argmax_out);
+    if (!claim_scratch(h, symbol, as_stream(stream))) {
+        return 1;
+    }
     return finish(h, symbol, kc::launch_lm_head_argmax(a, as_stream(stream)));
 }
 

@@ -323,6 +323,37 @@ def test_lm_head_argmax(torch_gpu, native, stream, vocab, with_norm):
     assert tok == int(np.argmax(lf))  # first maximum, as torch.argmax
 
 
+def test_handle_scratch_is_refused_to_a_second_busy_stream(torch_gpu, native, stream):
+    """The handle's scratch (here lm_head's block winners and ticket) serves
+    one stream at a time: a call on another stream is refused while the last
+    user's stream still has work queued, and accepted once it is idle."""
+    torch = torch_gpu
+    vocab = 4096
+    x = synthetic.f32_to_bf16_bits(synthetic.normal(SEED, (12,), (2048,), 1.0))
+    emb = synthetic.embedding_bits(SEED, vocab=vocab)
+    d_x, d_e = dev(torch, x), dev(torch, emb)
+    outs = [(empty(torch, vocab, "u16"), empty(torch, 1, "i32")) for _ in range(2)]
+    other = torch.cuda.Stream()
+    lib = native.lib
+
+    def lm_head(k, s):
+        return lib.kudacuda_lm_head_argmax_bf16(native.handle, p(d_x), 0, p(d_e), p(outs[k][0]), p(outs[k][1]), vocab,
+                                                 2048, 1.0e-6, s.cuda_stream)
+
+    stream.synchronize()
+    with torch.cuda.stream(stream):
+        torch.cuda._sleep(100_000_000)  # keeps the first stream busy (bounded spin, ~0.05 s)
+    assert lm_head(0, stream) == 0
+    assert lm_head(1, other) == 1 and "scratch" in native.error()
+    stream.synchronize()
+    assert lm_head(1, other) == 0
+    other.synchronize()
+    assert np.array_equal(host(outs[1][0]), host(outs[0][0]))
+    assert int(host(outs[1][1])[0]) == int(host(outs[0][1])[0])
+    assert lm_head(0, stream) == 0  # back on the first stream: the second is idle
+    stream.synchronize()
+
+
 def test_vector_add_and_rmsnorm_plumbing(torch_gpu, native, stream):
     torch = torch_gpu
     a = np.arange(1000, dtype=np.float32)

@@ -8,13 +8,16 @@
 //    1 KiB row (fully coalesced) and the lane's 32 activations stay in
 //    registers for every row the wave visits;
 //  * codes are looked up in a block-shared LDS table of code pairs (one
-//    8-byte entry per byte value), one byte-select shift per byte;
+//    8-byte entry per byte value), one byte-select shift per byte; gate/up,
+//    with one large block per CU, reads a lane-sliced copy (32 interleaved
+//    copies, one byte permute per byte) whose lookups never share a bank;
 //  * the RMSNorm is computed inside the consumer kernel: waves 0..3 of a
 //    block each normalise a quarter into LDS and every wave of the block
-//    (4, or 12 in gate/up) reads it, so no separate norm launch is needed;
+//    (4, or 11 in gate/up) reads it, so no separate norm launch is needed;
 //  * loads are issued in dependency order (activations, epilogue operands,
-//    rows), and gate/up requests its second task's rows only after its first
-//    task's dots (a wave stalled on a full memory queue stops in order);
+//    rows), and a gate/up wave requests task i + 1's rows only once task
+//    i's have arrived, then computes task i (a wave stalled on a full memory
+//    queue stops in order, its arithmetic with it);
 //  * reductions are wave64 butterflies on lane-swap and DPP instructions,
 //    two rows per chain.
 // Semantics follow the reference's tiled NF4 kernels

@@ -134,10 +134,11 @@ def test_prefill_emitting_the_stop_token_stops_the_decode(small_pair):
 
 @pytest.mark.parametrize("prompt_len,new,capacity", [(600, 24, 1024), (1030, 8, 2048)])
 def test_long_context_decode_matches_oracle(torch_gpu, native, prompt_len, new, capacity):
-    # Decode-step attention past the short-context regime: at 600+ cached
-    # tokens the flat path runs 19-20 splits of 32 tokens, more than o_proj
-    # merges, so the attention kernel's in-kernel merge runs; at 1030-1038
-    # tokens the flat path takes two tokens per group (64-token splits).
+    # Decode-step attention past the short-context regime: at 600-624 cached
+    # tokens the step's plan (at most 32 splits per KV head) makes 19-20
+    # one-round (32-token) splits, more than o_proj merges, so the attention
+    # kernel's ticket merge runs; at 1030-1038 tokens the splits grow to two
+    # rounds (64 tokens, 17 splits).
     kw = dict(num_layers=2, vocab=4096, kv_capacity=capacity, token_capacity=capacity)
     gpu = Qwen2Nf4Decoder.synthetic(native, torch_gpu, seed=SEED, **kw)
     cpu = HostModel(SEED, **kw)
@@ -152,11 +153,12 @@ def test_long_context_decode_matches_oracle(torch_gpu, native, prompt_len, new, 
 
 @pytest.mark.parametrize("start,capacity", [(2100, 4096), (4200, 8192)])
 def test_decode_from_a_seeded_long_cache_matches_oracle(torch_gpu, native, start, capacity):
-    # The round path inside the decode step: both models get the same
-    # random cache rows 0..start-1 and decode from position start.  At 2100+
-    # tokens the 128-token splits number 17-18, merged by the attention
-    # kernel's ticket; at 4200 of an 8192-row cache they number 33+, past the
-    # ticket, so the step's separate merge kernel runs.
+    # Longer splits inside the decode step: both models get the same random
+    # cache rows 0..start-1 and decode from position start.  At 2100+ tokens
+    # the step's plan makes 22 splits of three 32-token rounds, at 4200 of an
+    # 8192-row cache 27 splits of five rounds; both are merged by the
+    # attention kernel's ticket (the step's plan never exceeds 32 splits, so
+    # its graph holds no merge kernel).
     torch = torch_gpu
     new = 6
     kw = dict(num_layers=2, vocab=4096, kv_capacity=capacity, token_capacity=capacity)

@@ -221,7 +221,7 @@ def test_gqa_decode_bf16_config4(torch_gpu, native, stream, kv_len):
 
 @pytest.mark.parametrize("kv_len,capacity", [(1, 512), (100, 512), (512, 512), (33, 2048), (513, 2048), (585, 2048),
                                              (2048, 2048), (200, 32768), (8000, 32768), (8193, 32768),
-                                             (30001, 32768)])
+                                             (30001, 32768), (32768, 32768)])
 def test_gqa_graph_reads_device_kv_len(torch_gpu, native, stream, kv_len, capacity):
     torch = torch_gpu
     q, k, v = synthetic.gqa_inputs(SEED, kv_len, capacity)
@@ -233,6 +233,35 @@ def test_gqa_graph_reads_device_kv_len(torch_gpu, native, stream, kv_len, capaci
                 scale, p(d_len), stream.cuda_stream)
     stream.synchronize()
     assert np.array_equal(host(out), O.gqa(q, k, v, kv_len))
+
+
+@pytest.mark.parametrize("symbol,capacity,excess", [("kudacuda_qwen2_gqa_decode_graph_bf16", 2048, 1),
+                                                    ("kudacuda_qwen2_gqa_decode_graph_bf16", 2048, 100000),
+                                                    ("kudacuda_qwen2_gqa_decode_workspace_v3", 512, 37)])
+def test_gqa_device_kv_len_beyond_capacity_is_clamped(torch_gpu, native, stream, symbol, capacity, excess):
+    # a device kv_len past the cache's capacity reads the whole cache and no
+    # further, as the reference workspace kernel clamps it
+    # (qwen2_gqa_workspace.cuh:35-36)
+    torch = torch_gpu
+    q, k, v = synthetic.gqa_inputs(SEED + 5, capacity, capacity)
+    scale = synthetic.default_scale()
+    d_len = dev(torch, np.array([capacity + excess], dtype=np.int32))
+    out = empty(torch, 2048, "u16")
+    if symbol.endswith("workspace_v3"):
+        q = O.f32_to_f16(O.bf16_to_f32(q))
+        k, v = (O.f32_to_f16(O.bf16_to_f32(t)).reshape(2, capacity, 128) for t in (k, v))
+        d_q, d_k, d_v = dev(torch, q), dev(torch, k), dev(torch, v)
+        ws = empty(torch, 16 * 8 * 130, "f32")
+        native.call(symbol, p(d_q), p(d_k), p(d_v), p(out), p(ws), p(d_len), 1, 1, capacity, 16, 2, 128, scale,
+                    stream.cuda_stream)
+        stream.synchronize()
+        assert np.array_equal(host(out), O.gqa(q, k, v, capacity, scale=scale, dtype="f16", split_limit=8))
+    else:
+        d_q, d_k, d_v = dev(torch, q), dev(torch, k), dev(torch, v)
+        native.call(symbol, p(d_q), p(d_k), p(d_v), p(out), 1, 1, capacity, 16, 2, 128, scale, p(d_len),
+                    stream.cuda_stream)
+        stream.synchronize()
+        assert np.array_equal(host(out), O.gqa(q, k, v, capacity))
 
 
 @pytest.mark.parametrize("symbol", ["kudacuda_qwen2_gqa_decode", "kudacuda_qwen2_gqa_decode_group_tiled",

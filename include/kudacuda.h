@@ -15,8 +15,8 @@
  *   - one handle per host thread / stream: the handle's graph objects and its
  *     attention/argmax/GEMM scratch are not shared safely between concurrent
  *     calls; a call that uses that scratch on another stream than the last
- *     such call returns 1 while that stream still has work queued (captures
- *     are not checked).
+ *     such call returns 1 until that call's launch has completed (an event
+ *     the handle records behind it; captures are not checked).
  * Activations named "_bf16" are bfloat16; the reference's un-suffixed NF4 QKV
  * and GQA entry points keep their fp16 activations.
  */

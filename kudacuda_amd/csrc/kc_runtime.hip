@@ -90,6 +90,9 @@ struct Handle {
         if (scratch != nullptr) {
             (void)hipFree(scratch);
         }
+        if (scratch_event != nullptr) {
+            (void)hipEventDestroy(scratch_event);
+        }
     }
     void set_error(const std::string& message) { last_error = message; }
     void set_hip_error(const char* operation, hipError_t status) {
@@ -112,8 +115,10 @@ struct Handle {
     int32_t* argmax_slot = nullptr;
     // this device's copy of the file-scope `scratch` array (device address)
     unsigned char* static_scratch = nullptr;
-    // stream of the last call that used the handle's scratch (claim_scratch)
+    // the last scratch-using launch: its stream (compared, never queried)
+    // and an event recorded behind it (claim_scratch / scratch_launched)
     hipStream_t scratch_stream = nullptr;
+    hipEvent_t scratch_event = nullptr;
     bool scratch_used = false;
 };
 
@@ -139,32 +144,51 @@ bool ready(Handle* h, const char* symbol) {
 }
 
 // Calls that use the handle's scratch (split partials, ticket counters,
-// argmax winners, GEMM partials) must not overlap on the GPU.  A call on
-// another stream than the previous scratch user is refused while that stream
-// still has work queued, which may still be using the scratch; a call on the
-// same stream is ordered after it.  Launches into a stream capture are not
-// checked: they run when the graph is replayed (graphs are one per handle).
-bool claim_scratch(Handle* h, const char* symbol, hipStream_t s) {
+// argmax winners, GEMM partials) must not overlap on the GPU.  After each
+// such launch the handle records its own event on the launch's stream; a
+// call on another stream is refused while that event has not completed (the
+// previous launch may still be using the scratch).  Only the handle's event
+// is queried: the previous stream may have been destroyed since.  A call on
+// the same stream is ordered after the previous one.  Launches recorded into
+// a stream capture are not checked: they run when the graph is replayed.
+bool capturing(hipStream_t s) {
+    if (s == nullptr) {
+        return false;  // the legacy stream is never captured (and asking it during a global capture is unsafe)
+    }
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
+    const hipError_t q = hipStreamIsCapturing(s, &cs);
+    (void)hipGetLastError();
+    return q == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
+bool claim_scratch(Handle* h, const char* symbol, hipStream_t s) {
+    if (capturing(s) || !h->scratch_used || s == h->scratch_stream) {
         return true;
     }
-    if (h->scratch_used && s != h->scratch_stream) {
-        hipStreamCaptureStatus ps = hipStreamCaptureStatusNone;
-        const bool prev_capturing =
-            hipStreamIsCapturing(h->scratch_stream, &ps) == hipSuccess && ps != hipStreamCaptureStatusNone;
-        const hipError_t q = prev_capturing ? hipSuccess : hipStreamQuery(h->scratch_stream);
-        (void)hipGetLastError();  // a busy (or since destroyed) stream is an answer, not an error
-        if (q == hipErrorNotReady) {
-            h->set_error(std::string(symbol) +
-                         ": the handle's scratch is in use by work still queued on another stream; "
-                         "synchronise that stream first or use one handle per stream");
-            return false;
-        }
+    const hipError_t q = hipEventQuery(h->scratch_event);
+    (void)hipGetLastError();  // "not ready" is an answer, not an error
+    if (q == hipErrorNotReady) {
+        h->set_error(std::string(symbol) +
+                     ": the handle's scratch is in use by work still queued on another stream; "
+                     "synchronise that stream first or use one handle per stream");
+        return false;
+    }
+    return true;
+}
+
+// Records the handle's event behind a scratch-using launch (not into a
+// capture); passes the launch status through.
+hipError_t scratch_launched(Handle* h, hipStream_t s, hipError_t launch) {
+    if (launch != hipSuccess || capturing(s)) {
+        return launch;
+    }
+    const hipError_t rec = hipEventRecord(h->scratch_event, s);
+    if (rec != hipSuccess) {
+        return rec;
     }
     h->scratch_stream = s;
     h->scratch_used = true;
-    return true;
+    return hipSuccess;
 }
 
 int finish(Handle* h, const char* operation, hipError_t status) {
@@ -337,7 +361,7 @@ int gqa_direct(void* raw, const char* symbol, Act act, uint64_t q, uint64_t k, u
     if (!claim_scratch(h, symbol, as_stream(stream))) {
         return 1;
     }
-    return finish(h, symbol, launch_gqa_decode(act, a, as_stream(stream)));
+    return finish(h, symbol, scratch_launched(h, as_stream(stream), launch_gqa_decode(act, a, as_stream(stream))));
 }
 
 // no_alloc: split partials and counters come from this device's copy of the
@@ -384,7 +408,8 @@ int gqa_graph(void* raw, const char* symbol, Act act, uint64_t q, uint64_t k, ui
         }
     }
     a.qk_scale_log2 = s.scale * kLog2e;
-    return finish(h, symbol, launch_gqa_decode(act, a, as_stream(stream)));
+    const hipError_t launched = launch_gqa_decode(act, a, as_stream(stream));
+    return finish(h, symbol, no_alloc ? launched : scratch_launched(h, as_stream(stream), launched));
 }
 
 // ---------------------------------------------------------------- model
@@ -724,6 +749,7 @@ using kc::Handle;
 using kc::ptr;
 using kc::ready;
 using kc::claim_scratch;
+using kc::scratch_launched;
 
 extern "C" {
 
@@ -760,6 +786,12 @@ void* kudacuda_create(int device_id) {
     }
     if (status != hipSuccess) {
         h->set_hip_error("hipMemset(handle counters)", status);
+        return h;
+    }
+    status = hipEventCreateWithFlags(&h->scratch_event, hipEventDisableTiming);
+    if (status != hipSuccess) {
+        h->scratch_event = nullptr;
+        h->set_hip_error("hipEventCreateWithFlags(handle scratch event)", status);
         return h;
     }
     void* static_scratch = nullptr;
@@ -1093,7 +1125,7 @@ int kudacuda_nf4_gemm_bf16(void* raw, uint64_t input, uint64_t weight_packed, ui
     if (!claim_scratch(h, symbol, as_stream(stream))) {
         return 1;
     }
-    return finish(h, symbol, kc::gemm_chunks(epi, a, tokens, as_stream(stream)));
+    return finish(h, symbol, scratch_launched(h, as_stream(stream), kc::gemm_chunks(epi, a, tokens, as_stream(stream))));
 }
 
 int kudacuda_nf4_gemm_swiglu_bf16(void* raw, uint64_t input, uint64_t gate_weight_packed, uint64_t gate_absmax,
@@ -1126,7 +1158,8 @@ int kudacuda_nf4_gemm_swiglu_bf16(void* raw, uint64_t input, uint64_t gate_weigh
     if (!claim_scratch(h, symbol, as_stream(stream))) {
         return 1;
     }
-    return finish(h, symbol, kc::gemm_chunks(kc::GemmEpi::kSwiGlu, a, tokens, as_stream(stream)));
+    return finish(h, symbol,
+                  scratch_launched(h, as_stream(stream), kc::gemm_chunks(kc::GemmEpi::kSwiGlu, a, tokens, as_stream(stream))));
 }
 
 int kudacuda_nf4_quantize(void* raw, uint64_t input, int64_t input_dtype, int64_t count, int64_t blocksize,
@@ -1208,7 +1241,7 @@ int kudacuda_qwen2_gqa_decode_workspace_v3(void* raw, uint64_t query, uint64_t k
     if (!claim_scratch(h, symbol, as_stream(stream))) {
         return 1;
     }
-    return finish(h, symbol, kc::launch_gqa_decode(Act::kF16, a, as_stream(stream)));
+    return finish(h, symbol, scratch_launched(h, as_stream(stream), kc::launch_gqa_decode(Act::kF16, a, as_stream(stream))));
 }
 
 int kudacuda_qwen2_gqa_decode(void* raw, uint64_t query, uint64_t key_cache, uint64_t value_cache, uint64_t output,
@@ -1304,7 +1337,7 @@ int kudacuda_lm_head_argmax_bf16(void* raw, uint64_t input, uint64_t norm_weight
     if (!claim_scratch(h, symbol, as_stream(stream))) {
         return 1;
     }
-    return finish(h, symbol, kc::launch_lm_head_argmax(a, as_stream(stream)));
+    return finish(h, symbol, scratch_launched(h, as_stream(stream), kc::launch_lm_head_argmax(a, as_stream(stream))));
 }
 
 int64_t kudacuda_lm_head_workspace_floats(void) { return kc::lm_head_workspace_floats(); }

@@ -13,7 +13,7 @@
 //    copies, one byte permute per byte) whose lookups never share a bank;
 //  * the RMSNorm is computed inside the consumer kernel: waves 0..3 of a
 //    block each normalise a quarter into LDS and every wave of the block
-//    (4, or 11 in gate/up) reads it, so no separate norm launch is needed;
+//    (4, 7 in QKV+RoPE, 11 in gate/up) reads it, so no separate norm launch is needed;
 //  * loads are issued in dependency order (activations, epilogue operands,
 //    rows), and a gate/up wave requests task i + 1's rows only once task
 //    i's have arrived, then computes task i (a wave stalled on a full memory
@@ -40,6 +40,11 @@ constexpr int kRowsThreads = 256;
 // blocks of 4 tasks (8.2 us).
 constexpr int kSwiGluThreads = 704;
 constexpr int64_t kSwiGluWaves = 2816;
+// QKV+RoPE blocks: 7 waves (waves 0..3 compute the shared norm, 4..6 read
+// it), ~183 blocks.  Decode step, 10 interleaved runs of 128 steps on each of
+// two boxes: 1.1191 ms against 1.1215 for 4-wave blocks (5, 6, 8, 9 waves:
+// 1.1225, 1.1222, 1.1322, 1.1266).
+constexpr int kQkvRopeThreads = 448;
 constexpr int kNormPitch = 36;  // floats per lane row of the shared norm (32 + 4: conflict-free)
 // Launch cap of the other row kernels (GEMV, QKV): up to 6144 waves (24 per
 // CU on 256 CUs), one task per wave at the model's shapes; measured faster
@@ -671,6 +676,11 @@ hipError_t launch_rows_tpw(const Nf4RowsArgs& a, int64_t ntasks, int64_t blocks,
                            dim3(static_cast<unsigned>(blocks)), dim3(kSwiGluThreads), 0, stream, a, ntasks);
         return hipGetLastError();
     }
+    if constexpr (MODE == RowMode::kQkvRope) {
+        hipLaunchKernelGGL((nf4_rows2048_kernel<T, MODE, TPW, false, kQkvRopeThreads>),
+                           dim3(static_cast<unsigned>(blocks)), dim3(kQkvRopeThreads), 0, stream, a, ntasks);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL((nf4_rows2048_kernel<T, MODE, TPW>), dim3(static_cast<unsigned>(blocks)), dim3(kRowsThreads),
                        0, stream, a, ntasks);
     return hipGetLastError();
@@ -699,7 +709,8 @@ hipError_t launch_rows_t(const Nf4RowsArgs& a, hipStream_t stream) {
         }
     }
     // every wave's tasks in flight at once
-    const int64_t waves_per_block = (MODE == RowMode::kSwiGlu ? kSwiGluThreads : kRowsThreads) / 64;
+    const int64_t waves_per_block =
+        (MODE == RowMode::kSwiGlu ? kSwiGluThreads : (MODE == RowMode::kQkvRope ? kQkvRopeThreads : kRowsThreads)) / 64;
     const int64_t max_waves = MODE == RowMode::kSwiGlu ? kSwiGluWaves : kMaxRowWaves;
     int64_t tpw = (ntasks + max_waves - 1) / max_waves;
     tpw = tpw <= 1 ? 1 : (tpw <= 2 ? 2 : (tpw <= 4 ? 4 : 8));

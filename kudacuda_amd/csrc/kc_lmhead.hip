@@ -71,23 +71,16 @@ __global__ __launch_bounds__(kLmThreads) void lm_head_kernel(LmHeadArgs a) {
     float best = -__builtin_huge_valf();
     int32_t best_idx = 0x7fffffff;
     if (active) {
-        // Loads first, in a fixed order: the activation chunks (norm layout
-        // [32l, 32l+32) and dot layout 8(l + 64c) + j), gamma, then the first
-        // kRing rows of the ring, so the norm arithmetic overlaps the row
-        // loads and every wait is for a known prefix of the issued loads.
+        // Loads first, in a fixed order: the first kRing rows of the ring,
+        // then the activation chunks (norm layout [32l, 32l+32) and dot
+        // layout 8(l + 64c) + j) and gamma.  The rows' HBM requests go out
+        // ahead of the activation's L2 reads (decode step 1.1173 -> 1.1160 ms
+        // over 10 interleaved runs); every wait is for a known prefix of the
+        // issued loads, and the first dot needs its rows anyway.
         const uint4* xv = reinterpret_cast<const uint4*>(a.x);
         const bool has_gamma = a.gamma != nullptr;
         const uint4* gv = reinterpret_cast<const uint4*>(has_gamma ? a.gamma : a.x);
         uint4 xs_raw[4], xd_raw[4], g_raw[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            xs_raw[i] = xv[lane * 4 + i];
-        }
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            xd_raw[c] = xv[lane + 64 * c];
-            g_raw[c] = gv[lane + 64 * c];
-        }
 
         // Ring of kRing rows per wave: row base + i*nwaves sits in slot i and is
         // refilled with the row kRing*nwaves further on as soon as it has been
@@ -111,6 +104,15 @@ __global__ __launch_bounds__(kLmThreads) void lm_head_kernel(LmHeadArgs a) {
             }
         }
         __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            xs_raw[i] = xv[lane * 4 + i];
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            xd_raw[c] = xv[lane + 64 * c];
+            g_raw[c] = gv[lane + 64 * c];
+        }
 
         // Final RMSNorm: inverse RMS over elements [32l, 32l+32) per lane,
         // then the lane's dot elements normalised the same way.

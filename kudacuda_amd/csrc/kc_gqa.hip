@@ -190,7 +190,16 @@ __device__ __forceinline__ void ticket_merge(const GqaArgs& a, const float* part
 
 template <typename T>
 __global__ __launch_bounds__(kGqaThreads) __attribute__((amdgpu_waves_per_eu(4)))
-void gqa_partial_kernel(GqaArgs a) {
+void gqa_partial_kernel(const uint16_t* k_rows, const uint16_t* v_rows, const uint16_t* q_vec,
+                        const int32_t* kv_len_device, int64_t capacity, GqaArgs args) {
+    // the leading scalar arguments (what the first loads need) are preloaded
+    // into SGPRs at wave launch; they stand for the same fields of `args`
+    GqaArgs a = args;
+    a.k = k_rows;
+    a.v = v_rows;
+    a.q = q_vec;
+    a.kv_len_device = kv_len_device;
+    a.capacity = capacity;
     __shared__ __attribute__((aligned(16))) float s_vf[2][kRound][kDim];           // V rows of a round
     __shared__ __attribute__((aligned(16))) float s_sc[2][kHeadsPerGroup][kPitch];  // scores
     __shared__ __attribute__((aligned(16))) float s_wt[2][kHeadsPerGroup][kPitch];  // weights
@@ -572,9 +581,11 @@ hipError_t launch_gqa_decode(Act act, const GqaArgs& a, hipStream_t stream) {
     }
     const dim3 grid(static_cast<unsigned>(a.max_splits), 2);
     if (act == Act::kBf16) {
-        hipLaunchKernelGGL(gqa_partial_kernel<Bf16>, grid, dim3(kGqaThreads), 0, stream, a);
+        hipLaunchKernelGGL(gqa_partial_kernel<Bf16>, grid, dim3(kGqaThreads), 0, stream, a.k, a.v, a.q,
+                           a.kv_len_device, a.capacity, a);
     } else {
-        hipLaunchKernelGGL(gqa_partial_kernel<F16>, grid, dim3(kGqaThreads), 0, stream, a);
+        hipLaunchKernelGGL(gqa_partial_kernel<F16>, grid, dim3(kGqaThreads), 0, stream, a.k, a.v, a.q,
+                           a.kv_len_device, a.capacity, a);
     }
     hipError_t status = hipGetLastError();
     if (status != hipSuccess || a.max_splits <= a.ticket_max) {

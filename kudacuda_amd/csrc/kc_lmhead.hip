@@ -52,7 +52,15 @@ __device__ __forceinline__ float row_dot(const uint4* w, const float* xn) {
     return (a[0] + a[1]) + (a[2] + a[3]);
 }
 
-__global__ __launch_bounds__(kLmThreads) void lm_head_kernel(LmHeadArgs a) {
+// The leading scalar arguments (what the first loads need) are preloaded
+// into SGPRs at wave launch; they stand for the same fields of `args`.
+__global__ __launch_bounds__(kLmThreads) void lm_head_kernel(const uint16_t* weight, const uint16_t* x,
+                                                             const uint16_t* gamma, int64_t vocab, LmHeadArgs args) {
+    LmHeadArgs a = args;
+    a.weight = weight;
+    a.x = x;
+    a.gamma = gamma;
+    a.vocab = vocab;
     __shared__ float s_val[kLmThreads / 64];
     __shared__ int32_t s_idx[kLmThreads / 64];
     __shared__ int s_last;
@@ -272,7 +280,8 @@ hipError_t launch_lm_head_argmax(const LmHeadArgs& a, hipStream_t stream) {
     if (blocks < 1) {
         blocks = 1;
     }
-    hipLaunchKernelGGL(lm_head_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kLmThreads), 0, stream, a);
+    hipLaunchKernelGGL(lm_head_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kLmThreads), 0, stream, a.weight, a.x,
+                       a.gamma, a.vocab, a);
     return hipGetLastError();
 }
 

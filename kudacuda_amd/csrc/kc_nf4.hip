@@ -99,9 +99,17 @@ __device__ __forceinline__ RowPair map_task(const Nf4RowsArgs& a, int64_t task) 
     return p;
 }
 
+// Entry m of a three-pointer field by selects: the kernel's argument struct
+// is a local copy (its leading pointers come preloaded), and a runtime index
+// into one of its arrays would put the whole copy in scratch memory.
+template <typename P>
+__device__ __forceinline__ P pick3(const P (&arr)[3], int m) {
+    return m == 0 ? arr[0] : (m == 1 ? arr[1] : arr[2]);
+}
+
 __device__ __forceinline__ void fetch_row(const Nf4RowsArgs& a, int m, int64_t r, int lane, uint4& pk, float& am) {
-    pk = reinterpret_cast<const uint4*>(a.w[m] + r * 1024)[lane];
-    am = a.absmax[m][r * 32 + (lane >> 1)];
+    pk = reinterpret_cast<const uint4*>(pick3(a.w, m) + r * 1024)[lane];
+    am = pick3(a.absmax, m)[r * 32 + (lane >> 1)];
 }
 
 // wx[x] = lane x's value of every lane's 16-lane row, for x in X
@@ -131,8 +139,9 @@ __device__ __forceinline__ Epi fetch_epilogue(const Nf4RowsArgs& a, const RowPai
         e.b0 = *bias;
         e.res = *res;
     } else if constexpr (MODE == RowMode::kQkv || MODE == RowMode::kQkvRope) {
-        e.b0 = a.bias[p.m0][p.r0];
-        e.b1 = a.bias[p.m0][p.r1];
+        const uint16_t* bias = pick3(a.bias, p.m0);
+        e.b0 = bias[p.r0];
+        e.b1 = bias[p.r1];
         if constexpr (MODE == RowMode::kQkvRope) {
             const int64_t d = p.r0 & 127;
             e.c = a.rope_cos[pos * 64 + d];
@@ -167,8 +176,8 @@ __device__ __forceinline__ void row_epilogue(const Nf4RowsArgs& a, const RowPair
             const float v0 = d0 + T::load(e.b0);
             const float v1 = d1 + T::load(e.b1);
             if constexpr (MODE == RowMode::kQkv) {
-                a.out[m][cur.r0] = T::store(v0);
-                a.out[m][cur.r1] = T::store(v1);
+                pick3(a.out, m)[cur.r0] = T::store(v0);
+                pick3(a.out, m)[cur.r1] = T::store(v1);
             } else {
                 float o0 = v0, o1 = v1;
                 if (m < 2) {
@@ -190,6 +199,50 @@ __device__ __forceinline__ void row_epilogue(const Nf4RowsArgs& a, const RowPair
     }
 }
 
+// Fields of Nf4RowsArgs passed again as the row kernel's leading pointer
+// arguments, per mode: the weight rows and absmax, and what the mode loads
+// first besides (GEMV: the attention partials and length, x, residual;
+// SwiGLU: x and the norm weight).
+template <RowMode MODE>
+struct RowsHot {
+    static constexpr bool kQkvRows = MODE == RowMode::kQkv || MODE == RowMode::kQkvRope;
+    static void get(const Nf4RowsArgs& a, const void* (&h)[6]) {
+        if constexpr (MODE == RowMode::kGemv) {
+            h[0] = a.w[0], h[1] = a.absmax[0], h[2] = a.attn.partials, h[3] = a.attn.kv_len_device, h[4] = a.x,
+            h[5] = a.residual;
+        } else if constexpr (kQkvRows) {
+            h[0] = a.w[0], h[1] = a.w[1], h[2] = a.w[2], h[3] = a.absmax[0], h[4] = a.absmax[1], h[5] = a.absmax[2];
+        } else {
+            h[0] = a.w[0], h[1] = a.w[1], h[2] = a.absmax[0], h[3] = a.absmax[1], h[4] = a.x, h[5] = a.gamma;
+        }
+    }
+    __device__ __forceinline__ static void apply(Nf4RowsArgs& a, const void* h0, const void* h1, const void* h2,
+                                                 const void* h3, const void* h4, const void* h5) {
+        if constexpr (MODE == RowMode::kGemv) {
+            a.w[0] = static_cast<const uint8_t*>(h0);
+            a.absmax[0] = static_cast<const float*>(h1);
+            a.attn.partials = static_cast<const float*>(h2);
+            a.attn.kv_len_device = static_cast<const int32_t*>(h3);
+            a.x = static_cast<const uint16_t*>(h4);
+            a.residual = static_cast<const uint16_t*>(h5);
+        } else if constexpr (kQkvRows) {
+            a.w[0] = static_cast<const uint8_t*>(h0);
+            a.w[1] = static_cast<const uint8_t*>(h1);
+            a.w[2] = static_cast<const uint8_t*>(h2);
+            a.absmax[0] = static_cast<const float*>(h3);
+            a.absmax[1] = static_cast<const float*>(h4);
+            a.absmax[2] = static_cast<const float*>(h5);
+        } else {
+            a.w[0] = static_cast<const uint8_t*>(h0);
+            a.w[1] = static_cast<const uint8_t*>(h1);
+            a.absmax[0] = static_cast<const float*>(h2);
+            a.absmax[1] = static_cast<const float*>(h3);
+            a.x = static_cast<const uint16_t*>(h4);
+            a.gamma = static_cast<const uint16_t*>(h5);
+        }
+    }
+};
+
 // Each wave owns up to TPW tasks (task = gwave + i * nwaves).  Loads are
 // issued in one fixed order before any arithmetic: activation and norm
 // weight, epilogue operands, then every row of every task (tasks past the end
@@ -204,8 +257,16 @@ __device__ __forceinline__ void row_epilogue(const Nf4RowsArgs& a, const RowPair
 // the attention kernel's own merge -- into LDS before the block barrier.
 // The kv_len word, the partials and x (used when the attention merged
 // itself) are requested before the weight rows.
+//
+// The six leading pointer arguments are preloaded into SGPRs at wave launch
+// (the fields the first, longest loads need; RowsHot maps them per mode) and
+// stand for the same fields of `args`.
 template <typename T, RowMode MODE, int TPW, bool ATTN = false, int NTH = kRowsThreads>
-__global__ __launch_bounds__(NTH) void nf4_rows2048_kernel(Nf4RowsArgs a, int64_t ntasks) {
+__global__ __launch_bounds__(NTH) void nf4_rows2048_kernel(const void* h0, const void* h1, const void* h2,
+                                                           const void* h3, const void* h4, const void* h5,
+                                                           Nf4RowsArgs args, int64_t ntasks) {
+    Nf4RowsArgs a = args;
+    RowsHot<MODE>::apply(a, h0, h1, h2, h3, h4, h5);
     static_assert(!ATTN || MODE == RowMode::kGemv, "attention merge feeds the GEMV only");
     static_assert(!ATTN || kRowsThreads * 8 == 2048, "one thread per 8 merged outputs");
     // kQkv / kQkvRope / kSwiGlu: the block shares the RMSNorm (waves 0..3 each
@@ -522,7 +583,20 @@ __global__ __launch_bounds__(NTH) void nf4_rows2048_kernel(Nf4RowsArgs a, int64_
 // block's rows, then the R rows (lanes past the last chunk re-read it and
 // contribute 0).  Row total = sum of the W wave sums in wave order.
 template <typename T, int NCHUNK, int R>
-__global__ __launch_bounds__(64 * ((NCHUNK + 63) / 64)) void nf4_down_kernel(Nf4DownArgs a) {
+//
+// The arguments are scalars so that all of them are preloaded into SGPRs at
+// wave launch.
+__global__ __launch_bounds__(64 * ((NCHUNK + 63) / 64)) void nf4_down_kernel(const uint16_t* x, const uint8_t* w,
+                                                                            const float* absmax,
+                                                                            const uint16_t* residual, uint16_t* out,
+                                                                            int64_t rows) {
+    Nf4DownArgs a;
+    a.x = x;
+    a.w = w;
+    a.absmax = absmax;
+    a.residual = residual;
+    a.out = out;
+    a.rows = rows;
     constexpr int W = (NCHUNK + 63) / 64;
     // the pair table and one spare entry that threads past the table overwrite
     __shared__ __attribute__((aligned(16))) float cb[2 * kNf4PairEntries + 2];
@@ -664,25 +738,28 @@ __global__ __launch_bounds__(256) void nf4_dequantize_kernel(const uint8_t* pack
 
 template <typename T, RowMode MODE, int TPW>
 hipError_t launch_rows_tpw(const Nf4RowsArgs& a, int64_t ntasks, int64_t blocks, hipStream_t stream) {
+    const void* h[6];
+    RowsHot<MODE>::get(a, h);
+    const dim3 grid(static_cast<unsigned>(blocks));
     if constexpr (MODE == RowMode::kGemv && TPW == 1) {
         if (a.attn.partials != nullptr) {
-            hipLaunchKernelGGL((nf4_rows2048_kernel<T, MODE, TPW, true>), dim3(static_cast<unsigned>(blocks)),
-                               dim3(kRowsThreads), 0, stream, a, ntasks);
+            hipLaunchKernelGGL((nf4_rows2048_kernel<T, MODE, TPW, true>), grid, dim3(kRowsThreads), 0, stream, h[0],
+                               h[1], h[2], h[3], h[4], h[5], a, ntasks);
             return hipGetLastError();
         }
     }
     if constexpr (MODE == RowMode::kSwiGlu) {
-        hipLaunchKernelGGL((nf4_rows2048_kernel<T, MODE, TPW, false, kSwiGluThreads>),
-                           dim3(static_cast<unsigned>(blocks)), dim3(kSwiGluThreads), 0, stream, a, ntasks);
+        hipLaunchKernelGGL((nf4_rows2048_kernel<T, MODE, TPW, false, kSwiGluThreads>), grid, dim3(kSwiGluThreads), 0,
+                           stream, h[0], h[1], h[2], h[3], h[4], h[5], a, ntasks);
         return hipGetLastError();
     }
     if constexpr (MODE == RowMode::kQkvRope) {
-        hipLaunchKernelGGL((nf4_rows2048_kernel<T, MODE, TPW, false, kQkvRopeThreads>),
-                           dim3(static_cast<unsigned>(blocks)), dim3(kQkvRopeThreads), 0, stream, a, ntasks);
+        hipLaunchKernelGGL((nf4_rows2048_kernel<T, MODE, TPW, false, kQkvRopeThreads>), grid, dim3(kQkvRopeThreads),
+                           0, stream, h[0], h[1], h[2], h[3], h[4], h[5], a, ntasks);
         return hipGetLastError();
     }
-    hipLaunchKernelGGL((nf4_rows2048_kernel<T, MODE, TPW>), dim3(static_cast<unsigned>(blocks)), dim3(kRowsThreads),
-                       0, stream, a, ntasks);
+    hipLaunchKernelGGL((nf4_rows2048_kernel<T, MODE, TPW>), grid, dim3(kRowsThreads), 0, stream, h[0], h[1], h[2],
+                       h[3], h[4], h[5], a, ntasks);
     return hipGetLastError();
 }
 
@@ -762,10 +839,10 @@ hipError_t launch_nf4_down11008(Act act, const Nf4DownArgs& a, hipStream_t strea
     const int64_t blocks = (a.rows + kRows - 1) / kRows;
     if (act == Act::kBf16) {
         hipLaunchKernelGGL((nf4_down_kernel<Bf16, kChunks, kRows>), dim3(static_cast<unsigned>(blocks)),
-                           dim3(kThreads), 0, stream, a);
+                           dim3(kThreads), 0, stream, a.x, a.w, a.absmax, a.residual, a.out, a.rows);
     } else {
         hipLaunchKernelGGL((nf4_down_kernel<F16, kChunks, kRows>), dim3(static_cast<unsigned>(blocks)),
-                           dim3(kThreads), 0, stream, a);
+                           dim3(kThreads), 0, stream, a.x, a.w, a.absmax, a.residual, a.out, a.rows);
     }
     return hipGetLastError();
 }

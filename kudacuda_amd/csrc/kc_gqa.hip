@@ -471,8 +471,16 @@ __global__ __launch_bounds__(256) void gqa_merge_kernel(GqaArgs a) {
     const int h = blockIdx.x;
     const int d0 = blockIdx.y * kSlice;
     const int64_t L = read_kv_len(a);
-    const int nsplit = static_cast<int>(gqa_split_count(L, a.split_cap));
-    if (nsplit <= a.ticket_max) {
+    const int nsplit = static_cast<int>(a.mfma ? gqa_mfma_split_count(L, a.split_cap) : gqa_split_count(L, a.split_cap));
+    if (a.mfma) {
+        // the matrix-core partial kernel merges nothing itself
+        if (nsplit == 0) {
+            if (threadIdx.x < kSlice) {
+                a.out[static_cast<int64_t>(h) * kDim + d0 + threadIdx.x] = 0;  // empty cache
+            }
+            return;
+        }
+    } else if (nsplit <= a.ticket_max) {
         return;  // merged by the partial kernel
     }
     const float* src = a.partials + static_cast<int64_t>(h) * a.max_splits * kPartialStride;
@@ -558,6 +566,333 @@ __global__ __launch_bounds__(256) void gqa_merge_kernel(GqaArgs a) {
     }
 }
 
+// ------------------------------------------------------ matrix-core tactic
+// Grid (max_splits, 2), 4 waves.  Block (s, g) owns split s of KV head g
+// (gqa_mfma_split_tokens tokens); wave w takes the split's 32-token chunks
+// w, w + 4, ... and keeps its own online softmax over them; the four wave
+// results are merged in LDS into the split partial (max, sum, acc[128] per
+// head: the round path's layout), which gqa_merge_kernel combines.
+//
+// Operand layouts of v_mfma_f32_16x16x32 (lane l, r = l % 16, c = l / 16):
+// A[r][8c + j], B[8c + j][r], D[4c + i][r].  Per chunk:
+//   * scores S^T = K q^T over two 16-token tiles and 4 k-steps: A = K rows
+//     (lane l: token r of the tile, dims 32k + 8c .. +7, so one load
+//     instruction reads 64 contiguous bytes of each of 16 rows), B = q (lane
+//     l: query head r of the group, zero for r >= 8).  D leaves lane l the
+//     scores of head r for tokens 4c + i (tile 0) and 16 + 4c + i (tile 1);
+//   * online softmax: the chunk maximum over the lane's 8 scores and the 4
+//     lanes of head r (lane swaps at distance 32 and 16), weights
+//     w = exp2(s - m'), rescale exp2(m - m'); each lane keeps its own running
+//     sum of w (rescaled alike), the 4 lanes of a head are added at the end;
+//   * P.V as D = P V: A = P with k slot 8c + j holding the lane's own tokens
+//     (j < 4 tile 0, j >= 4 tile 1), so the scores' output layout is the
+//     weights' input layout and nothing moves between lanes.  P enters as two
+//     MFMAs, its 16-bit rounding hi and the rounding of the remainder w - hi,
+//     which carries ~16 significant bits of each fp32 weight.  B = V^T in
+//     the same slot order, staged in the wave's own LDS region (row = dim,
+//     80-byte rows: the 16 lanes of one B read fall on distinct banks);
+//     acc (lane l: heads 4c + i at dim 16t + r of dim tile t) is rescaled per
+//     head first, with factors read from lanes 0..7.
+// Rows past the split's end are loaded clamped to its last row, their scores
+// are -inf and their V is zeroed, so every load stays in bounds and nothing
+// past the cache end reaches a sum.  The waves of a block exchange data only
+// through LDS; a wave's own V^T stores and reads are ordered by the LDS
+// executing one wave's instructions in issue order.
+typedef __bf16 mfma_bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 mfma_f16x8 __attribute__((ext_vector_type(8)));
+typedef float mfma_f32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+struct MfmaOps;
+template <>
+struct MfmaOps<Bf16> {
+    typedef mfma_bf16x8 vec;
+    static __device__ __forceinline__ mfma_f32x4 mac(vec a, vec b, mfma_f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ void split(const float* w, vec& hi, vec& lo) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const __bf16 h = static_cast<__bf16>(w[j]);
+            hi[j] = h;
+            lo[j] = static_cast<__bf16>(w[j] - static_cast<float>(h));
+        }
+    }
+};
+template <>
+struct MfmaOps<F16> {
+    typedef mfma_f16x8 vec;
+    static __device__ __forceinline__ mfma_f32x4 mac(vec a, vec b, mfma_f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ void split(const float* w, vec& hi, vec& lo) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const _Float16 h = static_cast<_Float16>(w[j]);
+            hi[j] = h;
+            lo[j] = static_cast<_Float16>(w[j] - static_cast<float>(h));
+        }
+    }
+};
+
+constexpr int kMfmaWaves = 4;
+constexpr int kMfmaThreads = 64 * kMfmaWaves;
+constexpr int kChunk = 32;
+static_assert(kMfmaWaves * kChunk == kGqaMfmaQuantum, "a split unit is one chunk per wave");
+static_assert(kGqaMfmaSplitCap <= kMergeMaxSplits, "the merge kernel takes every split");
+constexpr int kVtPitch = 40;  // 16-bit slots per staged V^T row (80 bytes)
+
+struct MfmaChunk {
+    uint4 k[2][4];  // K: tile, k-step
+    uint4 v[4][2];  // V: token 4va + i, dims 16vb + 8h .. +7
+};
+
+__device__ __forceinline__ float lane_swap_max(float v) {
+    const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(p32[0]), __uint_as_float(p32[1]));
+    const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(p16[0]), __uint_as_float(p16[1]));
+}
+__device__ __forceinline__ float lane_swap_sum(float v) {
+    const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
+    const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
+}
+
+// kPer: chunks per wave of a split (gqa_mfma_split_tokens / 128) when the
+// host knows it (1 or 2: every load is issued up front in straight-line code,
+// so each chunk waits only for its own rows); 0: any count, chunks requested
+// one pair ahead in a loop.
+template <typename T, int kPer>
+__global__ __launch_bounds__(kMfmaThreads) void gqa_mfma_partial_kernel(GqaArgs a) {
+    using Ops = MfmaOps<T>;
+    typedef typename Ops::vec vec;
+    __shared__ __attribute__((aligned(16))) uint16_t s_vt[kMfmaWaves][kDim * kVtPitch];
+    __shared__ float s_m[kMfmaWaves][kHeadsPerGroup];
+    __shared__ float s_l[kMfmaWaves][kHeadsPerGroup];
+    static_assert(kMfmaWaves * kDim * kHeadsPerGroup * sizeof(float) <= sizeof(s_vt), "wave results fit the V stage");
+
+    const int g = blockIdx.y;
+    const int s = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int r = lane & 15;
+    const int c = lane >> 4;
+
+    // q first (every lane loads a row of the group; lanes r >= 8 then clear
+    // theirs with a mask, so the loads stay unconditional and in order)
+    vec bq[4];
+    {
+        const uint16_t* qrow = a.q + (g * kHeadsPerGroup + (r & 7)) * kDim + 8 * c;
+        const uint32_t keep = r < kHeadsPerGroup ? 0xffffffffu : 0u;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            uint4 v = *reinterpret_cast<const uint4*>(qrow + 32 * k);
+            v.x &= keep;
+            v.y &= keep;
+            v.z &= keep;
+            v.w &= keep;
+            bq[k] = __builtin_bit_cast(vec, v);
+        }
+    }
+
+    const int L = static_cast<int>(read_kv_len(a));
+    const int C = static_cast<int>(gqa_mfma_split_tokens(L, a.split_cap));
+    const int nsplit = static_cast<int>(gqa_mfma_split_count(L, a.split_cap));
+    if (s >= nsplit) {
+        return;
+    }
+    const int t0 = s * C;
+    const int tend = t0 + C < L ? t0 + C : L;
+    const int last = tend - 1;
+    const int nchunk = (tend - t0 + kChunk - 1) / kChunk;
+    const int64_t head_off = static_cast<int64_t>(g) * a.capacity * kDim;
+    const uint16_t* kbase = a.k + head_off + 8 * c;
+    const int va = lane >> 3;  // token quad of the lane's V loads
+    const int vb = lane & 7;   // 16-dim block of the lane's V loads
+    const uint16_t* vbase = a.v + head_off + 16 * vb;
+
+    auto load_chunk = [&](int ci, MfmaChunk& ch) {
+        const int tb = t0 + kChunk * ci;
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+            const int row = tb + 16 * x + r < last ? tb + 16 * x + r : last;
+            const uint16_t* p = kbase + row * kDim;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                ch.k[x][k] = *reinterpret_cast<const uint4*>(p + 32 * k);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = tb + 4 * va + i < last ? tb + 4 * va + i : last;
+            const uint16_t* p = vbase + row * kDim;
+            ch.v[i][0] = *reinterpret_cast<const uint4*>(p);
+            ch.v[i][1] = *reinterpret_cast<const uint4*>(p + 8);
+        }
+    };
+
+    MfmaChunk ca, cb;
+    load_chunk(wave, ca);
+    if constexpr (kPer != 1) {
+        load_chunk(wave + kMfmaWaves, cb);
+    }
+
+    uint16_t* vt = s_vt[wave];
+    const int sb = va < 4 ? 8 * va : 8 * (va - 4) + 4;  // k slot of the lane's first V token
+    float m_run = kNegInf;
+    float lsum = 0.0f;
+    mfma_f32x4 acc[kDim / 16];
+#pragma unroll
+    for (int t = 0; t < kDim / 16; ++t) {
+        acc[t] = mfma_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+
+    auto process = [&](int ci, const MfmaChunk& ch) {
+        const int tb = t0 + kChunk * ci;
+        const int nv = tend - tb < kChunk ? tend - tb : kChunk;
+        // V^T stage: for each dim, the lane's 4 tokens as 4 consecutive slots
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            uint32_t wv[4][4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const bool live = 4 * va + i < nv;
+                wv[i][0] = live ? ch.v[i][h].x : 0u;
+                wv[i][1] = live ? ch.v[i][h].y : 0u;
+                wv[i][2] = live ? ch.v[i][h].z : 0u;
+                wv[i][3] = live ? ch.v[i][h].w : 0u;
+            }
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const int d = 16 * vb + 8 * h + 2 * m;
+                const uint2 even = make_uint2((wv[0][m] & 0xffffu) | (wv[1][m] << 16), (wv[2][m] & 0xffffu) | (wv[3][m] << 16));
+                const uint2 odd = make_uint2((wv[0][m] >> 16) | (wv[1][m] & 0xffff0000u),
+                                             (wv[2][m] >> 16) | (wv[3][m] & 0xffff0000u));
+                *reinterpret_cast<uint2*>(vt + d * kVtPitch + sb) = even;
+                *reinterpret_cast<uint2*>(vt + (d + 1) * kVtPitch + sb) = odd;
+            }
+        }
+        mfma_f32x4 d0 = {0.0f, 0.0f, 0.0f, 0.0f};
+        mfma_f32x4 d1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            d0 = Ops::mac(__builtin_bit_cast(vec, ch.k[0][k]), bq[k], d0);
+            d1 = Ops::mac(__builtin_bit_cast(vec, ch.k[1][k]), bq[k], d1);
+        }
+        float sc[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sc[i] = 4 * c + i < nv ? d0[i] * a.qk_scale_log2 : kNegInf;
+            sc[4 + i] = 16 + 4 * c + i < nv ? d1[i] * a.qk_scale_log2 : kNegInf;
+        }
+        float cm = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+        cm = lane_swap_max(cm);
+        const float m_new = fmaxf(m_run, cm);
+        // a chunk past the split's end (nv <= 0) with nothing before it leaves
+        // m at -inf: exponents are taken against 0 then, so all weights and the
+        // rescale are exactly 0 instead of NaN
+        const float m_ref = m_new == kNegInf ? 0.0f : m_new;
+        const float cr = __builtin_amdgcn_exp2f(m_run - m_ref);
+        float w[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            w[j] = __builtin_amdgcn_exp2f(sc[j] - m_ref);
+        }
+        lsum = fmaf(lsum, cr, ((w[0] + w[1]) + (w[2] + w[3])) + ((w[4] + w[5]) + (w[6] + w[7])));
+        m_run = m_new;
+        vec phi, plo;
+        Ops::split(w, phi, plo);
+        float crh[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cr), i));
+            const float hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cr), 4 + i));
+            crh[i] = c == 0 ? lo : hi;
+        }
+        __asm__ volatile("" ::: "memory");  // the V^T stores above precede the B reads
+#pragma unroll
+        for (int t = 0; t < kDim / 16; ++t) {
+            const uint4 bv = *reinterpret_cast<const uint4*>(vt + (16 * t + r) * kVtPitch + 8 * c);
+            mfma_f32x4 x = acc[t];
+            x[0] *= crh[0];
+            x[1] *= crh[1];
+            x[2] *= crh[2];
+            x[3] *= crh[3];
+            x = Ops::mac(phi, __builtin_bit_cast(vec, bv), x);
+            x = Ops::mac(plo, __builtin_bit_cast(vec, bv), x);
+            acc[t] = x;
+        }
+        __asm__ volatile("" ::: "memory");  // and the next chunk's stores follow them
+    };
+
+    // a wave's chunks: wave, wave + 4, ... (< nchunk).  With kPer fixed every
+    // chunk is processed unconditionally (one past the end adds nothing), so
+    // the compiler keeps its loads ahead of the first wait instead of sinking
+    // them into a branch.
+    if constexpr (kPer == 1) {
+        process(wave, ca);
+    } else if constexpr (kPer == 2) {
+        process(wave, ca);
+        process(wave + kMfmaWaves, cb);
+    } else {
+        // the two register sets alternate; the chunk after next is requested
+        // as soon as a set is free (clamped rows, so unconditionally)
+#pragma unroll 1
+        for (int ci = wave; ci < nchunk; ci += 2 * kMfmaWaves) {
+            process(ci, ca);
+            load_chunk(ci + 2 * kMfmaWaves, ca);
+            if (ci + kMfmaWaves >= nchunk) {
+                break;
+            }
+            process(ci + kMfmaWaves, cb);
+            load_chunk(ci + 3 * kMfmaWaves, cb);
+        }
+    }
+    lsum = lane_swap_sum(lsum);
+
+    __syncthreads();  // every wave is done with its V^T stage
+    float* s_acc = reinterpret_cast<float*>(&s_vt[0][0]);  // [wave][dim][head]
+    if (c < 2) {
+#pragma unroll
+        for (int t = 0; t < kDim / 16; ++t) {
+            *reinterpret_cast<float4*>(s_acc + ((wave * kDim + 16 * t + r) * kHeadsPerGroup + 4 * c)) =
+                make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+        }
+    }
+    if (lane < kHeadsPerGroup) {
+        s_m[wave][lane] = m_run;
+        s_l[wave][lane] = lsum;
+    }
+    __syncthreads();
+    // thread: dim d of heads 4hq .. 4hq + 3; the waves in order
+    const int d = threadIdx.x & (kDim - 1);
+    const int hq = threadIdx.x >> 7;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int h = 4 * hq + i;
+        float M = s_m[0][h];
+#pragma unroll
+        for (int w = 1; w < kMfmaWaves; ++w) {
+            M = fmaxf(M, s_m[w][h]);
+        }
+        float o = 0.0f;
+        float lt = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kMfmaWaves; ++w) {
+            const float ww = __builtin_amdgcn_exp2f(s_m[w][h] - M);
+            o = fmaf(s_acc[(w * kDim + d) * kHeadsPerGroup + h], ww, o);
+            lt = fmaf(s_l[w][h], ww, lt);
+        }
+        float* dst = a.partials + (static_cast<int64_t>(g * kHeadsPerGroup + h) * a.max_splits + s) * kPartialStride;
+        dst[2 + d] = o;
+        if (d == 0) {
+            *reinterpret_cast<float2*>(dst) = make_float2(M, lt);
+        }
+    }
+}
+
 }  // namespace
 
 GqaPlan gqa_plan(int64_t capacity, int64_t split_limit) {
@@ -589,6 +924,43 @@ hipError_t launch_gqa_decode(Act act, const GqaArgs& a, hipStream_t stream) {
     }
     hipError_t status = hipGetLastError();
     if (status != hipSuccess || a.max_splits <= a.ticket_max) {
+        return status;
+    }
+    const dim3 mgrid(16, kDim / kMergeDims);
+    if (act == Act::kBf16) {
+        hipLaunchKernelGGL(gqa_merge_kernel<Bf16>, mgrid, dim3(256), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL(gqa_merge_kernel<F16>, mgrid, dim3(256), 0, stream, a);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gqa_decode_mfma(Act act, GqaArgs a, hipStream_t stream) {
+    a.mfma = true;
+    // the grid must cover every split of the length a host-length call names,
+    // or of any length up to the capacity when the length is in device memory
+    const int64_t units = (a.capacity + kGqaMfmaQuantum - 1) / kGqaMfmaQuantum;
+    const int64_t host_len = a.kv_len_host < 0 ? 0 : (a.kv_len_host > a.capacity ? a.capacity : a.kv_len_host);
+    const int64_t need = a.kv_len_device == nullptr ? gqa_mfma_split_count(host_len, a.split_cap)
+                                                     : (units < a.split_cap ? units : a.split_cap);
+    if (a.capacity <= 0 || a.capacity > (int64_t{1} << 24) || a.split_cap <= 0 || a.split_cap > kGqaMfmaSplitCap ||
+        a.max_splits < need || a.max_splits > kMergeMaxSplits) {
+        return hipErrorInvalidValue;
+    }
+    const dim3 grid(static_cast<unsigned>(a.max_splits), 2);
+    // chunks per wave: fixed by the host length, else any
+    const int64_t per = a.kv_len_device == nullptr ? gqa_mfma_split_tokens(host_len, a.split_cap) / kGqaMfmaQuantum : 0;
+    if (act == Act::kBf16) {
+        auto* kernel = per == 1 ? gqa_mfma_partial_kernel<Bf16, 1>
+                                : (per == 2 ? gqa_mfma_partial_kernel<Bf16, 2> : gqa_mfma_partial_kernel<Bf16, 0>);
+        hipLaunchKernelGGL(kernel, grid, dim3(kMfmaThreads), 0, stream, a);
+    } else {
+        auto* kernel = per == 1 ? gqa_mfma_partial_kernel<F16, 1>
+                                : (per == 2 ? gqa_mfma_partial_kernel<F16, 2> : gqa_mfma_partial_kernel<F16, 0>);
+        hipLaunchKernelGGL(kernel, grid, dim3(kMfmaThreads), 0, stream, a);
+    }
+    hipError_t status = hipGetLastError();
+    if (status != hipSuccess) {
         return status;
     }
     const dim3 mgrid(16, kDim / kMergeDims);

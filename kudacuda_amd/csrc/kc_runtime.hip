@@ -25,6 +25,11 @@ namespace kc {
 namespace {
 
 constexpr int64_t kMaxStandaloneKv = 65536;
+// Direct calls (kv_len known on the host) at this many cached tokens or more
+// take the matrix-core tactic (MI355X, cold cache, us per call, round path vs
+// matrix cores: 4096 8.5 / 9.7, 8192 10.2 / 10.0, 16384 13.1 / 11.1, 32768
+// 17.5 / 13.4).
+constexpr int64_t kGqaMfmaMinKv = 8192;
 constexpr int64_t kMaxModelKv = 32768;
 
 // ------------------------------------------------ allocation-free scratch
@@ -360,6 +365,13 @@ int gqa_direct(void* raw, const char* symbol, Act act, uint64_t q, uint64_t k, u
     a.qk_scale_log2 = s.scale * kLog2e;
     if (!claim_scratch(h, symbol, as_stream(stream))) {
         return 1;
+    }
+    if (kv_len >= kGqaMfmaMinKv) {
+        // long caches: the matrix-core tactic (scores and weighted sum on MFMA)
+        a.split_cap = kGqaMfmaSplitCap;
+        a.max_splits = gqa_mfma_split_count(kv_len, a.split_cap);
+        return finish(h, symbol,
+                      scratch_launched(h, as_stream(stream), launch_gqa_decode_mfma(act, a, as_stream(stream))));
     }
     return finish(h, symbol, scratch_launched(h, as_stream(stream), launch_gqa_decode(act, a, as_stream(stream))));
 }

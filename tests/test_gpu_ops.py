@@ -193,11 +193,34 @@ def test_mlp_config3(torch_gpu, native, stream, with_norm, with_residual):
     _close(host(out), y)
 
 
-# one-round (32-token) splits up to 8192 tokens: finished in place up to 32,
-# ticket merge up to 4 splits (128), merge kernel beyond, with one merge group
-# up to 512 and more past it; splits of 2, 3 and 4 rounds past 8192, 16384
-# and 24576 tokens (256 splits per KV head at 32768)
-KV_LENS = [1, 7, 32, 33, 37, 128, 129, 511, 512, 513, 585, 1024, 2048, 2049, 8192, 8193, 16385, 32768]
+# Round path (bit-exact to the oracle): one-round (32-token) splits, finished
+# in place up to 32 tokens, ticket merge up to 4 splits (128), merge kernel
+# beyond, with one merge group up to 512 and more past it.  From
+# MFMA_MIN_KV on, direct calls take the matrix-core tactic (splits of 128
+# tokens, 2 chunks per wave past 16384, the generic chunk loop past 32768).
+KV_LENS = [1, 7, 32, 33, 37, 128, 129, 511, 512, 513, 585, 1024, 2048, 2049, 8191, 8192, 8193, 16385, 32768,
+           65536]
+MFMA_MIN_KV = 8192  # kGqaMfmaMinKv of kc_runtime.hip
+
+
+def _matrix_core_parity(got: np.ndarray, q, k, v, kv_len: int, scale: float, dtype: str) -> None:
+    """The matrix-core tactic sums in another order than the round path, with
+    the weights entering as a 16-bit hi + lo pair.  Every output must lie
+    within one step of the output dtype (at the reference's magnitude) plus
+    2^-20 -- the fp32 accumulation error of a softmax average, which decides
+    near zero -- of the fp64 result, and within twice that of the round-path
+    oracle.  A dropped token, split or rescale is far outside either bound."""
+
+    to32 = O.bf16_to_f32 if dtype == "bf16" else O.f16_to_f32
+    ref = R.gqa_f64(to32(q), to32(k).reshape(2, kv_len, 128), to32(v).reshape(2, kv_len, 128), kv_len, scale)
+    _close(got, ref, dtype)
+    rounded = O.f32_to_act(ref.astype(np.float32), dtype)
+    step = np.abs(to32((rounded + 1).astype(np.uint16)).astype(np.float64) - to32(rounded).astype(np.float64))
+    value = to32(got).astype(np.float64)
+    err = np.abs(value - ref)
+    assert (err <= step + 2.0**-20).all(), f"max error {err.max():.3e}, {(err > step + 2.0**-20).sum()} outside"
+    oracle = to32(O.gqa(q, k, v, kv_len, scale=scale, dtype=dtype)).astype(np.float64)
+    assert (np.abs(value - oracle) <= step + 2.0**-19).all()
 
 
 @pytest.mark.parametrize("kv_len", KV_LENS)
@@ -211,6 +234,9 @@ def test_gqa_decode_bf16_config4(torch_gpu, native, stream, kv_len):
                 stream.cuda_stream)
     stream.synchronize()
     got = host(out)
+    if kv_len >= MFMA_MIN_KV:
+        _matrix_core_parity(got, q, k, v, kv_len, scale, "bf16")
+        return
     assert np.array_equal(got, O.gqa(q, k, v, kv_len))
     ref = R.gqa_f64(O.bf16_to_f32(q), O.bf16_to_f32(k).reshape(2, kv_len, 128),
                     O.bf16_to_f32(v).reshape(2, kv_len, 128), kv_len, scale)
@@ -284,6 +310,20 @@ def test_gqa_fp16_reference_entry_points(torch_gpu, native, stream, symbol):
     assert np.array_equal(got, O.gqa(q, k, v, kv_len, scale=scale, dtype="f16"))
     ref = R.gqa_f64(O.f16_to_f32(q), O.f16_to_f32(k), O.f16_to_f32(v), kv_len, scale)
     assert np.abs(O.f16_to_f32(got) - ref).max() <= 3.5e-3  # the smoke test's tolerance
+
+
+@pytest.mark.parametrize("kv_len", [8192, 9000])
+def test_gqa_fp16_long_cache_matrix_cores(torch_gpu, native, stream, kv_len):
+    torch = torch_gpu
+    q32, k32, v32 = (O.bf16_to_f32(x) for x in synthetic.gqa_inputs(SEED + 1, kv_len))
+    q, k, v = O.f32_to_f16(q32), O.f32_to_f16(k32), O.f32_to_f16(v32)
+    d_q, d_k, d_v = dev(torch, q), dev(torch, k), dev(torch, v)
+    out = empty(torch, 2048, "u16")
+    scale = synthetic.default_scale()
+    native.call("kudacuda_qwen2_gqa_decode", p(d_q), p(d_k), p(d_v), p(out), 1, 1, kv_len, 16, 2, 128, scale,
+                stream.cuda_stream)
+    stream.synchronize()
+    _matrix_core_parity(host(out), q, k, v, kv_len, scale, "f16")
 
 
 def test_gqa_workspace_v3(torch_gpu, native, stream):

@@ -24,7 +24,7 @@ import ctypes
 import json
 import math
 import sys
-from dataclasses import dataclass
+from dataclasses import dataclass, fields
 from functools import wraps
 from pathlib import Path
 from types import MethodType
@@ -76,21 +76,30 @@ def select_library_name(platform_name: Optional[str] = None) -> str:
     return "libkudacuda.dylib" if name == "darwin" else "libkudacuda.so"
 
 
+# Required top-level manifest keys and the JSON type each must have (None:
+# any); the error texts name the type as the manifest schema does.
+_MANIFEST_SCHEMA: tuple[tuple[str, Optional[type]], ...] = (
+    ("target_arch", None),
+    ("implemented_tactics", list),
+    ("contracts", dict),
+)
+_JSON_KIND = {list: "a list", dict: "an object"}
+
+
 def load_manifest(path: str | Path) -> dict[str, Any]:
     """Read a tactic manifest and check its required keys and their types."""
 
     manifest_path = Path(path)
-    with manifest_path.open("r", encoding="utf-8") as handle:
-        manifest = json.load(handle)
+    manifest = json.loads(manifest_path.read_text(encoding="utf-8"))
     if not isinstance(manifest, dict):
         raise ValueError(f"Manifest must contain a JSON object: {manifest_path}")
-    for key in ("target_arch", "implemented_tactics", "contracts"):
-        if key not in manifest:
-            raise ValueError(f"Manifest missing required key '{key}': {manifest_path}")
-    if not isinstance(manifest["implemented_tactics"], list):
-        raise ValueError("Manifest 'implemented_tactics' must be a list")
-    if not isinstance(manifest["contracts"], dict):
-        raise ValueError("Manifest 'contracts' must be an object")
+    absent = [key for key, _ in _MANIFEST_SCHEMA if key not in manifest]
+    if absent:
+        raise ValueError(f"Manifest missing required key '{absent[0]}': {manifest_path}")
+    wrong = [(key, kind) for key, kind in _MANIFEST_SCHEMA if kind is not None and not isinstance(manifest[key], kind)]
+    if wrong:
+        key, kind = wrong[0]
+        raise ValueError(f"Manifest '{key}' must be {_JSON_KIND[kind]}")
     return manifest
 
 
@@ -104,9 +113,55 @@ def _shape(tensor: Any) -> tuple[int, ...]:
     return tuple(int(v) for v in getattr(tensor, "shape", ()))
 
 
-def _optional_int(mapping: Mapping[str, Any], key: str) -> Optional[int]:
-    value = mapping.get(key)
-    return None if value is None else int(value)
+def _on_device(tensor: Any) -> bool:
+    # PyTorch-ROCm reports HIP tensors as is_cuda
+    return bool(getattr(tensor, "is_cuda", False))
+
+
+def _call_or(tensor: Any, method: str, default: Any) -> Any:
+    """tensor.method() when the tensor has that method, else default."""
+
+    bound = getattr(tensor, method, None)
+    return bound() if callable(bound) else default
+
+
+def _is_contiguous(tensor: Any) -> bool:
+    return bool(_call_or(tensor, "is_contiguous", False))
+
+
+def _rank(tensor: Any) -> int:
+    return int(_call_or(tensor, "dim", -1))
+
+
+def _tensor_rules(tensor: Any, *, layout: Optional[str], dtype: Optional[str], rank: Optional[int] = None,
+                  count_min: Optional[int] = None, shape: Optional[tuple[int, ...]] = None):
+    """The checks a contract makes of one tensor, cheapest first, as a lazy
+    sequence of booleans (the caller stops at the first False).  A None
+    parameter is not checked."""
+
+    yield _on_device(tensor)
+    yield layout != "contiguous" or _is_contiguous(tensor)
+    yield dtype is None or _normalize_dtype(getattr(tensor, "dtype", "")) == dtype
+    yield rank is None or _rank(tensor) == rank
+    yield count_min is None or int(_call_or(tensor, "numel", -1)) >= count_min
+    yield shape is None or _shape(tensor) == shape
+
+
+def _contract_kwargs(cls: type, mapping: Mapping[str, Any], *, required: bool) -> dict[str, Any]:
+    """Constructor arguments of a contract dataclass from a manifest entry: the
+    text fields normalised (dtype names, lower-case layout), the rest ints;
+    with required=False an absent or empty text field and an absent number
+    become None."""
+
+    text = {"dtype": _normalize_dtype, "layout": lambda v: str(v).lower()}
+    out: dict[str, Any] = {}
+    for field in fields(cls):
+        value = mapping[field.name] if required else mapping.get(field.name)
+        if field.name in text:
+            out[field.name] = text[field.name](value) if (required or value) else None
+        else:
+            out[field.name] = None if value is None else int(value)
+    return out
 
 
 @dataclass(frozen=True)
@@ -122,37 +177,19 @@ class TensorContract:
 
     @classmethod
     def from_mapping(cls, mapping: Mapping[str, Any]) -> "TensorContract":
-        return cls(
-            dtype=_normalize_dtype(mapping["dtype"]) if mapping.get("dtype") else None,
-            layout=str(mapping["layout"]).lower() if mapping.get("layout") else None,
-            rank=_optional_int(mapping, "rank"),
-            batch_size=_optional_int(mapping, "batch_size"),
-            seq_len=_optional_int(mapping, "seq_len"),
-            count_min=_optional_int(mapping, "count_min"),
-        )
+        return cls(**_contract_kwargs(cls, mapping, required=False))
 
     def matches_shape(self, batch_size: int, seq_len: int) -> bool:
-        for declared, actual in ((self.batch_size, batch_size), (self.seq_len, seq_len)):
-            if declared is not None and actual != declared:
-                return False
-        return batch_size > 0 and seq_len > 0
+        pairs = ((self.batch_size, batch_size), (self.seq_len, seq_len))
+        return all(actual > 0 and declared in (None, actual) for declared, actual in pairs)
 
     def matches_tensor(self, tensor: Any) -> bool:
-        if tensor is None:
-            return True
-        if not _on_device(tensor):
-            return False
-        if self.layout == "contiguous" and not _is_contiguous(tensor):
-            return False
-        if self.dtype is not None and _normalize_dtype(getattr(tensor, "dtype", "")) != self.dtype:
-            return False
-        if self.rank is not None and _rank(tensor) != self.rank:
-            return False
-        if self.count_min is not None:
-            numel = getattr(tensor, "numel", None)
-            if not callable(numel) or int(numel()) < self.count_min:
-                return False
-        return True
+        return tensor is None or all(
+            _tensor_rules(tensor, layout=self.layout, dtype=self.dtype, rank=self.rank, count_min=self.count_min))
+
+
+# the one grouped-query geometry the kernels serve: (query heads, KV heads, head_dim)
+_GQA_GEOMETRY = (16, 2, 128)
 
 
 @dataclass(frozen=True)
@@ -172,54 +209,34 @@ class Qwen2GqaContract:
 
     @classmethod
     def from_mapping(cls, mapping: Mapping[str, Any]) -> "Qwen2GqaContract":
-        ints = {key: int(mapping[key]) for key in ("batch_size", "query_len", "kv_len_min", "kv_len_max",
-                                                    "query_heads", "kv_heads", "head_dim")}
-        return cls(dtype=_normalize_dtype(mapping["dtype"]), layout=str(mapping["layout"]).lower(), **ints)
+        return cls(**_contract_kwargs(cls, mapping, required=True))
 
     def matches(self, batch_size: int, query_len: int, kv_len: int) -> bool:
-        if (self.query_heads, self.kv_heads, self.head_dim) != (16, 2, 128):
-            return False
-        return (int(batch_size) == self.batch_size and int(query_len) == self.query_len
-                and self.kv_len_min <= int(kv_len) <= self.kv_len_max)
+        served = (self.query_heads, self.kv_heads, self.head_dim) == _GQA_GEOMETRY
+        call = (int(batch_size), int(query_len))
+        return served and call == (self.batch_size, self.query_len) and self.kv_len_min <= int(kv_len) <= self.kv_len_max
 
     def matches_tensor(self, tensor: Any, expected_shape: tuple[int, ...]) -> bool:
-        if not _on_device(tensor):
-            return False
-        if self.layout == "contiguous" and not _is_contiguous(tensor):
-            return False
-        return _normalize_dtype(getattr(tensor, "dtype", "")) == self.dtype and _shape(tensor) == expected_shape
-
-
-def _on_device(tensor: Any) -> bool:
-    # PyTorch-ROCm reports HIP tensors as is_cuda
-    return bool(getattr(tensor, "is_cuda", False))
-
-
-def _is_contiguous(tensor: Any) -> bool:
-    check = getattr(tensor, "is_contiguous", None)
-    return callable(check) and bool(check())
-
-
-def _rank(tensor: Any) -> int:
-    dim = getattr(tensor, "dim", None)
-    return int(dim()) if callable(dim) else -1
+        return all(_tensor_rules(tensor, layout=self.layout, dtype=self.dtype, shape=tuple(expected_shape)))
 
 
 def _qwen2_attention_dimensions(module: Any) -> tuple[int, int, int]:
-    """(query heads, kv heads, head_dim) from the module or its config."""
+    """(query heads, kv heads, head_dim): the module's own attribute where
+    Transformers sets one, else its config's; head_dim falls back to
+    hidden_size / heads."""
 
     config = getattr(module, "config", None)
-    heads = getattr(module, "num_heads", None)
-    if heads is None:
-        heads = getattr(config, "num_attention_heads", 0)
-    kv_heads = getattr(module, "num_key_value_heads", None)
-    if kv_heads is None:
-        kv_heads = getattr(config, "num_key_value_heads", 0)
+
+    def attribute(own: str, from_config: str) -> Any:
+        value = getattr(module, own, None)
+        return getattr(config, from_config, 0) if value is None else value
+
+    heads = int(attribute("num_heads", "num_attention_heads"))
+    kv_heads = int(attribute("num_key_value_heads", "num_key_value_heads"))
     head_dim = getattr(module, "head_dim", None)
     if head_dim is None:
-        hidden = int(getattr(config, "hidden_size", 0))
-        head_dim = hidden // int(heads) if heads else 0
-    return int(heads), int(kv_heads), int(head_dim)
+        head_dim = int(getattr(config, "hidden_size", 0)) // heads if heads else 0
+    return heads, kv_heads, int(head_dim)
 
 
 # positional parameters of Qwen2Attention.forward after hidden_states

@@ -108,7 +108,7 @@ __global__ __launch_bounds__(kLmThreads) void lm_head_kernel(const uint16_t* wei
             const uint4* src = wbase + (first + i * nwaves < last_row ? first + i * nwaves : last_row) * 256;
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                w[i][c] = src[64 * c];
+                w[i][c] = load_stream(src + 64 * c);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -151,7 +151,7 @@ __global__ __launch_bounds__(kLmThreads) void lm_head_kernel(const uint16_t* wei
                 const uint4* src = wbase + (rn < last_row ? rn : last_row) * 256;
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
-                    w[i][c] = src[64 * c];
+                    w[i][c] = load_stream(src + 64 * c);
                 }
                 // keep slot i's refill ahead of slot i+1's dot
                 __builtin_amdgcn_sched_barrier(0);

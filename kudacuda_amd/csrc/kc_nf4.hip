@@ -108,8 +108,8 @@ __device__ __forceinline__ P pick3(const P (&arr)[3], int m) {
 }
 
 __device__ __forceinline__ void fetch_row(const Nf4RowsArgs& a, int m, int64_t r, int lane, uint4& pk, float& am) {
-    pk = reinterpret_cast<const uint4*>(pick3(a.w, m) + r * 1024)[lane];
-    am = pick3(a.absmax, m)[r * 32 + (lane >> 1)];
+    pk = load_stream(reinterpret_cast<const uint4*>(pick3(a.w, m) + r * 1024) + lane);
+    am = load_stream(pick3(a.absmax, m) + r * 32 + (lane >> 1));
 }
 
 // wx[x] = lane x's value of every lane's 16-lane row, for x in X
@@ -634,8 +634,8 @@ __global__ __launch_bounds__(64 * ((NCHUNK + 63) / 64)) void nf4_down_kernel(con
     for (int i = 0; i < R; ++i) {
         __builtin_amdgcn_sched_barrier(0);
         const int64_t r = rbase + i < last_row ? rbase + i : last_row;
-        pk[i] = wv[r * row_chunks];
-        am[i] = a.absmax[r * row_blocks + (cc >> 1)];
+        pk[i] = load_stream(wv + r * row_chunks);
+        am[i] = load_stream(a.absmax + r * row_blocks + (cc >> 1));
     }
     __builtin_amdgcn_sched_barrier(0);
 

@@ -593,6 +593,7 @@ __global__ __launch_bounds__(256) void gqa_merge_kernel(GqaArgs a) {
 //     80-byte rows: the 16 lanes of one B read fall on distinct banks);
 //     acc (lane l: heads 4c + i at dim 16t + r of dim tile t) is rescaled per
 //     head first, with factors read from lanes 0..7.
+// K/V rows are read once per call and streamed (non-temporal loads).
 // Rows past the split's end are loaded clamped to its last row, their scores
 // are -inf and their V is zeroed, so every load stays in bounds and nothing
 // past the cache end reaches a sum.  The waves of a block exchange data only
@@ -721,15 +722,15 @@ __global__ __launch_bounds__(kMfmaThreads) void gqa_mfma_partial_kernel(GqaArgs 
             const uint16_t* p = kbase + row * kDim;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                ch.k[x][k] = *reinterpret_cast<const uint4*>(p + 32 * k);
+                ch.k[x][k] = load_stream(reinterpret_cast<const uint4*>(p + 32 * k));
             }
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = tb + 4 * va + i < last ? tb + 4 * va + i : last;
             const uint16_t* p = vbase + row * kDim;
-            ch.v[i][0] = *reinterpret_cast<const uint4*>(p);
-            ch.v[i][1] = *reinterpret_cast<const uint4*>(p + 8);
+            ch.v[i][0] = load_stream(reinterpret_cast<const uint4*>(p));
+            ch.v[i][1] = load_stream(reinterpret_cast<const uint4*>(p + 8));
         }
     };
 

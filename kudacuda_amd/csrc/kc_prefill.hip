@@ -99,7 +99,7 @@ __device__ __forceinline__ u32x16 x_fetch(const uint16_t* const* xrow, int xcol,
 
 __device__ __forceinline__ u32x8 w_fetch(const uint8_t* wrow, const float* arow, int64_t kw, int q) {
     const int64_t kq = kw + 32 * q;
-    const uint4 t = *reinterpret_cast<const uint4*>(wrow + kq / 2);
+    const uint4 t = load_stream(reinterpret_cast<const uint4*>(wrow + kq / 2));  // read once: streamed
     u32x8 v = {};
     v[0] = t.x;
     v[1] = t.y;

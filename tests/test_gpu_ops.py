@@ -8,6 +8,8 @@ rounding.  Inputs are the BASELINE configs, seeded.
 
 from __future__ import annotations
 
+import math
+
 import numpy as np
 import pytest
 
@@ -310,6 +312,37 @@ def test_gqa_fp16_reference_entry_points(torch_gpu, native, stream, symbol):
     assert np.array_equal(got, O.gqa(q, k, v, kv_len, scale=scale, dtype="f16"))
     ref = R.gqa_f64(O.f16_to_f32(q), O.f16_to_f32(k), O.f16_to_f32(v), kv_len, scale)
     assert np.abs(O.f16_to_f32(got) - ref).max() <= 3.5e-3  # the smoke test's tolerance
+
+
+@pytest.mark.parametrize("kv_len,needle", [(8192, 0), (8192, 4100), (9001, 9000), (32768, 20001)])
+def test_gqa_matrix_cores_needle_returns_its_value_row(torch_gpu, native, stream, kv_len, needle):
+    """One key whose score exceeds every other by >= 72 (log2 units) takes all
+    the weight: every other weight is below 2^-72, far under one fp32 step
+    of the output, so each head's output is that token's V row exactly --
+    whichever split and chunk hold it, and whatever the other splits hold."""
+    torch = torch_gpu
+    rng = np.random.default_rng(SEED + needle)
+    scale = synthetic.default_scale()
+    u = rng.standard_normal((2, 128)).astype(np.float32)
+    u /= np.linalg.norm(u, axis=1, keepdims=True)
+    q32 = np.repeat(u, 8, axis=0) * np.float32(8.0)             # the 8 heads of a group share q
+    k32 = rng.standard_normal((2, kv_len, 128)).astype(np.float32) * np.float32(0.01)
+    # score (log2 units) = 8 |u|^2 alpha scale log2(e) = 80 for the needle
+    k32[:, needle] = u * np.float32(10.0 / (scale * math.log2(math.e)))
+    v32 = rng.standard_normal((2, kv_len, 128)).astype(np.float32)
+    q, k, v = O.f32_to_bf16(q32), O.f32_to_bf16(k32), O.f32_to_bf16(v32)
+    d_q, d_k, d_v = dev(torch, q), dev(torch, k), dev(torch, v)
+    out = empty(torch, 2048, "u16")
+    native.call("kudacuda_qwen2_gqa_decode_bf16", p(d_q), p(d_k), p(d_v), p(out), 1, 1, kv_len, 16, 2, 128, scale,
+                stream.cuda_stream)
+    stream.synchronize()
+    got = host(out).reshape(16, 128)
+    # the needle's log2-domain score really is >= 72 above every other key's
+    qk = np.einsum("gd,gtd->gt", O.bf16_to_f32(q).reshape(16, 128)[::8].astype(np.float64),
+                   O.bf16_to_f32(k).astype(np.float64)) * scale * math.log2(math.e)
+    others = np.delete(qk, needle, axis=1)
+    assert (qk[:, needle] - others.max(axis=1)).min() >= 72.0
+    assert np.array_equal(got, np.repeat(v[:, needle], 8, axis=0))
 
 
 @pytest.mark.parametrize("kv_len", [8192, 9000])

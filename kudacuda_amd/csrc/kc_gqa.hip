@@ -471,7 +471,8 @@ __global__ __launch_bounds__(256) void gqa_merge_kernel(GqaArgs a) {
     const int h = blockIdx.x;
     const int d0 = blockIdx.y * kSlice;
     const int64_t L = read_kv_len(a);
-    const int nsplit = static_cast<int>(a.mfma ? gqa_mfma_split_count(L, a.split_cap) : gqa_split_count(L, a.split_cap));
+    const int nsplit = static_cast<int>(a.mfma ? gqa_mfma_split_count(L, a.split_cap, a.mfma_quantum)
+                                                : gqa_split_count(L, a.split_cap));
     if (a.mfma) {
         // the matrix-core partial kernel merges nothing itself
         if (nsplit == 0) {
@@ -567,10 +568,10 @@ __global__ __launch_bounds__(256) void gqa_merge_kernel(GqaArgs a) {
 }
 
 // ------------------------------------------------------ matrix-core tactic
-// Grid (max_splits, 2), 4 waves.  Block (s, g) owns split s of KV head g
-// (gqa_mfma_split_tokens tokens); wave w takes the split's 32-token chunks
-// w, w + 4, ... and keeps its own online softmax over them; the four wave
-// results are merged in LDS into the split partial (max, sum, acc[128] per
+// Grid (max_splits, 2), kWaves (2 or 4) waves.  Block (s, g) owns split s of
+// KV head g (gqa_mfma_split_tokens tokens, a multiple of 32 kWaves); wave w
+// takes the split's 32-token chunks w, w + kWaves, ... and keeps its own
+// online softmax over them; the wave results are merged in LDS into the split partial (max, sum, acc[128] per
 // head: the round path's layout), which gqa_merge_kernel combines.
 //
 // Operand layouts of v_mfma_f32_16x16x32 (lane l, r = l % 16, c = l / 16):
@@ -636,10 +637,7 @@ struct MfmaOps<F16> {
     }
 };
 
-constexpr int kMfmaWaves = 4;
-constexpr int kMfmaThreads = 64 * kMfmaWaves;
-constexpr int kChunk = 32;
-static_assert(kMfmaWaves * kChunk == kGqaMfmaQuantum, "a split unit is one chunk per wave");
+constexpr int kChunk = 32;  // tokens per wave step; a split unit is one chunk per wave
 static_assert(kGqaMfmaSplitCap <= kMergeMaxSplits, "the merge kernel takes every split");
 constexpr int kVtPitch = 40;  // 16-bit slots per staged V^T row (80 bytes)
 
@@ -661,18 +659,20 @@ __device__ __forceinline__ float lane_swap_sum(float v) {
     return __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
 }
 
-// kPer: chunks per wave of a split (gqa_mfma_split_tokens / 128) when the
+// kPer: chunks per wave of a split (gqa_mfma_split_tokens / quantum) when the
 // host knows it (1 or 2: every load is issued up front in straight-line code,
 // so each chunk waits only for its own rows); 0: any count, chunks requested
 // one pair ahead in a loop.
-template <typename T, int kPer>
-__global__ __launch_bounds__(kMfmaThreads) void gqa_mfma_partial_kernel(GqaArgs a) {
+template <typename T, int kPer, int kWaves>
+__global__ __launch_bounds__(64 * kWaves) void gqa_mfma_partial_kernel(GqaArgs a) {
     using Ops = MfmaOps<T>;
     typedef typename Ops::vec vec;
-    __shared__ __attribute__((aligned(16))) uint16_t s_vt[kMfmaWaves][kDim * kVtPitch];
-    __shared__ float s_m[kMfmaWaves][kHeadsPerGroup];
-    __shared__ float s_l[kMfmaWaves][kHeadsPerGroup];
-    static_assert(kMfmaWaves * kDim * kHeadsPerGroup * sizeof(float) <= sizeof(s_vt), "wave results fit the V stage");
+    constexpr int kThreads = 64 * kWaves;
+    static_assert(kWaves == 2 || kWaves == 4, "merge layout: 128 or 256 threads");
+    __shared__ __attribute__((aligned(16))) uint16_t s_vt[kWaves][kDim * kVtPitch];
+    __shared__ float s_m[kWaves][kHeadsPerGroup];
+    __shared__ float s_l[kWaves][kHeadsPerGroup];
+    static_assert(kWaves * kDim * kHeadsPerGroup * sizeof(float) <= sizeof(s_vt), "wave results fit the V stage");
 
     const int g = blockIdx.y;
     const int s = blockIdx.x;
@@ -699,8 +699,8 @@ __global__ __launch_bounds__(kMfmaThreads) void gqa_mfma_partial_kernel(GqaArgs 
     }
 
     const int L = static_cast<int>(read_kv_len(a));
-    const int C = static_cast<int>(gqa_mfma_split_tokens(L, a.split_cap));
-    const int nsplit = static_cast<int>(gqa_mfma_split_count(L, a.split_cap));
+    const int C = static_cast<int>(gqa_mfma_split_tokens(L, a.split_cap, kChunk * kWaves));
+    const int nsplit = static_cast<int>(gqa_mfma_split_count(L, a.split_cap, kChunk * kWaves));
     if (s >= nsplit) {
         return;
     }
@@ -737,7 +737,7 @@ __global__ __launch_bounds__(kMfmaThreads) void gqa_mfma_partial_kernel(GqaArgs 
     MfmaChunk ca, cb;
     load_chunk(wave, ca);
     if constexpr (kPer != 1) {
-        load_chunk(wave + kMfmaWaves, cb);
+        load_chunk(wave + kWaves, cb);
     }
 
     uint16_t* vt = s_vt[wave];
@@ -836,19 +836,19 @@ __global__ __launch_bounds__(kMfmaThreads) void gqa_mfma_partial_kernel(GqaArgs 
         process(wave, ca);
     } else if constexpr (kPer == 2) {
         process(wave, ca);
-        process(wave + kMfmaWaves, cb);
+        process(wave + kWaves, cb);
     } else {
         // the two register sets alternate; the chunk after next is requested
         // as soon as a set is free (clamped rows, so unconditionally)
 #pragma unroll 1
-        for (int ci = wave; ci < nchunk; ci += 2 * kMfmaWaves) {
+        for (int ci = wave; ci < nchunk; ci += 2 * kWaves) {
             process(ci, ca);
-            load_chunk(ci + 2 * kMfmaWaves, ca);
-            if (ci + kMfmaWaves >= nchunk) {
+            load_chunk(ci + 2 * kWaves, ca);
+            if (ci + kWaves >= nchunk) {
                 break;
             }
-            process(ci + kMfmaWaves, cb);
-            load_chunk(ci + 3 * kMfmaWaves, cb);
+            process(ci + kWaves, cb);
+            load_chunk(ci + 3 * kWaves, cb);
         }
     }
     lsum = lane_swap_sum(lsum);
@@ -867,21 +867,24 @@ __global__ __launch_bounds__(kMfmaThreads) void gqa_mfma_partial_kernel(GqaArgs 
         s_l[wave][lane] = lsum;
     }
     __syncthreads();
-    // thread: dim d of heads 4hq .. 4hq + 3; the waves in order
+    // thread: dim d of heads 4hq .. 4hq + 3 (both quads with 128 threads);
+    // the waves in order
     const int d = threadIdx.x & (kDim - 1);
-    const int hq = threadIdx.x >> 7;
+#pragma unroll
+    for (int hi = 0; hi < 8; hi += kThreads / kDim * 4) {
+    const int hq = (threadIdx.x >> 7) + hi / 4;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int h = 4 * hq + i;
         float M = s_m[0][h];
 #pragma unroll
-        for (int w = 1; w < kMfmaWaves; ++w) {
+        for (int w = 1; w < kWaves; ++w) {
             M = fmaxf(M, s_m[w][h]);
         }
         float o = 0.0f;
         float lt = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kMfmaWaves; ++w) {
+        for (int w = 0; w < kWaves; ++w) {
             const float ww = __builtin_amdgcn_exp2f(s_m[w][h] - M);
             o = fmaf(s_acc[(w * kDim + d) * kHeadsPerGroup + h], ww, o);
             lt = fmaf(s_l[w][h], ww, lt);
@@ -891,6 +894,7 @@ __global__ __launch_bounds__(kMfmaThreads) void gqa_mfma_partial_kernel(GqaArgs 
         if (d == 0) {
             *reinterpret_cast<float2*>(dst) = make_float2(M, lt);
         }
+    }
     }
 }
 
@@ -940,9 +944,12 @@ hipError_t launch_gqa_decode_mfma(Act act, GqaArgs a, hipStream_t stream) {
     a.mfma = true;
     // the grid must cover every split of the length a host-length call names,
     // or of any length up to the capacity when the length is in device memory
-    const int64_t units = (a.capacity + kGqaMfmaQuantum - 1) / kGqaMfmaQuantum;
+    if (a.mfma_quantum != 64 && a.mfma_quantum != 128) {
+        return hipErrorInvalidValue;
+    }
+    const int64_t units = (a.capacity + a.mfma_quantum - 1) / a.mfma_quantum;
     const int64_t host_len = a.kv_len_host < 0 ? 0 : (a.kv_len_host > a.capacity ? a.capacity : a.kv_len_host);
-    const int64_t need = a.kv_len_device == nullptr ? gqa_mfma_split_count(host_len, a.split_cap)
+    const int64_t need = a.kv_len_device == nullptr ? gqa_mfma_split_count(host_len, a.split_cap, a.mfma_quantum)
                                                      : (units < a.split_cap ? units : a.split_cap);
     if (a.capacity <= 0 || a.capacity > (int64_t{1} << 24) || a.split_cap <= 0 || a.split_cap > kGqaMfmaSplitCap ||
         a.max_splits < need || a.max_splits > kMergeMaxSplits) {
@@ -950,15 +957,23 @@ hipError_t launch_gqa_decode_mfma(Act act, GqaArgs a, hipStream_t stream) {
     }
     const dim3 grid(static_cast<unsigned>(a.max_splits), 2);
     // chunks per wave: fixed by the host length, else any
-    const int64_t per = a.kv_len_device == nullptr ? gqa_mfma_split_tokens(host_len, a.split_cap) / kGqaMfmaQuantum : 0;
+    const int64_t per = a.kv_len_device == nullptr
+                            ? gqa_mfma_split_tokens(host_len, a.split_cap, a.mfma_quantum) / a.mfma_quantum
+                            : 0;
+    const bool two = a.mfma_quantum == 64;
+    const dim3 block(two ? 128 : 256);
     if (act == Act::kBf16) {
-        auto* kernel = per == 1 ? gqa_mfma_partial_kernel<Bf16, 1>
-                                : (per == 2 ? gqa_mfma_partial_kernel<Bf16, 2> : gqa_mfma_partial_kernel<Bf16, 0>);
-        hipLaunchKernelGGL(kernel, grid, dim3(kMfmaThreads), 0, stream, a);
+        auto* kernel = two ? (per == 1 ? gqa_mfma_partial_kernel<Bf16, 1, 2>
+                                       : (per == 2 ? gqa_mfma_partial_kernel<Bf16, 2, 2> : gqa_mfma_partial_kernel<Bf16, 0, 2>))
+                           : (per == 1 ? gqa_mfma_partial_kernel<Bf16, 1, 4>
+                                       : (per == 2 ? gqa_mfma_partial_kernel<Bf16, 2, 4> : gqa_mfma_partial_kernel<Bf16, 0, 4>));
+        hipLaunchKernelGGL(kernel, grid, block, 0, stream, a);
     } else {
-        auto* kernel = per == 1 ? gqa_mfma_partial_kernel<F16, 1>
-                                : (per == 2 ? gqa_mfma_partial_kernel<F16, 2> : gqa_mfma_partial_kernel<F16, 0>);
-        hipLaunchKernelGGL(kernel, grid, dim3(kMfmaThreads), 0, stream, a);
+        auto* kernel = two ? (per == 1 ? gqa_mfma_partial_kernel<F16, 1, 2>
+                                       : (per == 2 ? gqa_mfma_partial_kernel<F16, 2, 2> : gqa_mfma_partial_kernel<F16, 0, 2>))
+                           : (per == 1 ? gqa_mfma_partial_kernel<F16, 1, 4>
+                                       : (per == 2 ? gqa_mfma_partial_kernel<F16, 2, 4> : gqa_mfma_partial_kernel<F16, 0, 4>));
+        hipLaunchKernelGGL(kernel, grid, block, 0, stream, a);
     }
     hipError_t status = hipGetLastError();
     if (status != hipSuccess) {

@@ -59,19 +59,23 @@ __host__ __device__ inline int64_t gqa_split_count(int64_t L, int64_t split_cap)
     return static_cast<int64_t>((static_cast<uint32_t>(L) + c - 1) / c);
 }
 
-// Matrix-core tactic for long caches: splits are whole multiples of
-// kGqaMfmaQuantum tokens (4 waves x 32-token chunks), at most kGqaMfmaSplitCap
-// per KV head, chosen by the same fewest-whole-units rule.
+// Matrix-core tactic for long caches: splits are whole multiples of a
+// quantum of 32 tokens per wave of the partial kernel's block (128: 4-wave
+// blocks; 64: 2-wave blocks), at most kGqaMfmaSplitCap per KV head, chosen
+// by the same fewest-whole-units rule.
 constexpr int kGqaMfmaQuantum = 128;
 constexpr int64_t kGqaMfmaSplitCap = 128;
-__host__ __device__ inline int64_t gqa_mfma_split_tokens(int64_t L, int64_t split_cap) {
-    const uint32_t units = (static_cast<uint32_t>(L) + kGqaMfmaQuantum - 1) / kGqaMfmaQuantum;
+__host__ __device__ inline int64_t gqa_mfma_split_tokens(int64_t L, int64_t split_cap,
+                                                         int64_t quantum = kGqaMfmaQuantum) {
+    const uint32_t q = static_cast<uint32_t>(quantum);
+    const uint32_t units = (static_cast<uint32_t>(L) + q - 1) / q;
     const uint32_t cap = static_cast<uint32_t>(split_cap);
     const uint32_t per = (units + cap - 1) / cap;
-    return static_cast<int64_t>(kGqaMfmaQuantum) * (per > 1 ? per : 1);
+    return static_cast<int64_t>(q) * (per > 1 ? per : 1);
 }
-__host__ __device__ inline int64_t gqa_mfma_split_count(int64_t L, int64_t split_cap) {
-    const uint32_t c = static_cast<uint32_t>(gqa_mfma_split_tokens(L, split_cap));
+__host__ __device__ inline int64_t gqa_mfma_split_count(int64_t L, int64_t split_cap,
+                                                        int64_t quantum = kGqaMfmaQuantum) {
+    const uint32_t c = static_cast<uint32_t>(gqa_mfma_split_tokens(L, split_cap, quantum));
     return static_cast<int64_t>((static_cast<uint32_t>(L) + c - 1) / c);
 }
 
@@ -235,14 +239,15 @@ struct GqaArgs {
     int64_t ticket_max = 16;
     float qk_scale_log2 = 0.0f;    // scale * log2(e)
     bool mfma = false;             // split plan of the matrix-core tactic (gqa_mfma_split_tokens)
+    int64_t mfma_quantum = kGqaMfmaQuantum;  // its split unit: 64 (2-wave blocks) or 128 (4-wave blocks)
 };
 hipError_t launch_gqa_decode(Act act, const GqaArgs& args, hipStream_t stream);
 // Matrix-core tactic (v_mfma_f32_16x16x32_{bf16,f16} for q.K and P.V, the
 // weights P as a hi + lo pair of 16-bit values): partial kernel with
-// gqa_mfma_split_tokens(kv_len, split_cap) tokens per split, then
-// gqa_merge_kernel.  Results agree with the round path to fp32 rounding, not
+// gqa_mfma_split_tokens(kv_len, split_cap, mfma_quantum) tokens per split,
+// then gqa_merge_kernel.  Results agree with the round path to fp32 rounding, not
 // bit for bit.  Sets args.mfma itself; max_splits must cover
-// gqa_mfma_split_count(capacity, split_cap).
+// gqa_mfma_split_count(capacity, split_cap, mfma_quantum).
 hipError_t launch_gqa_decode_mfma(Act act, GqaArgs args, hipStream_t stream);
 // Split plan for a cache of `capacity` rows; split_limit > 0 caps the number
 // of splits (a caller-sized workspace).  Rule shared with the host oracle.

@@ -369,7 +369,10 @@ int gqa_direct(void* raw, const char* symbol, Act act, uint64_t q, uint64_t k, u
     if (kv_len >= kGqaMfmaMinKv) {
         // long caches: the matrix-core tactic (scores and weighted sum on MFMA)
         a.split_cap = kGqaMfmaSplitCap;
-        a.max_splits = gqa_mfma_split_count(kv_len, a.split_cap);
+        // 2-wave blocks (64-token units) while one unit per split fits the
+        // cap: twice the blocks of 4-wave ones to spread the stream over
+        a.mfma_quantum = kv_len <= 64 * kGqaMfmaSplitCap ? 64 : kGqaMfmaQuantum;
+        a.max_splits = gqa_mfma_split_count(kv_len, a.split_cap, a.mfma_quantum);
         return finish(h, symbol,
                       scratch_launched(h, as_stream(stream), launch_gqa_decode_mfma(act, a, as_stream(stream))));
     }

@@ -1,7 +1,14 @@
 // Split-KV grouped-query decode attention for the Qwen2.5-3B shape
-// (16 query heads, 2 KV heads, group 8, head_dim 128).
+// (16 query heads, 2 KV heads, group 8, head_dim 128), in two tactics:
+//   * the round path (below): fp32 FMA rounds, every summation order fixed
+//     and mirrored by the host oracle bit for bit; all graph-mode calls, the
+//     decode step and direct calls under 8192 cached tokens;
+//   * the matrix-core tactic (gqa_mfma_partial_kernel, further down): q.K and
+//     P.V on MFMA for direct calls from 8192 tokens on, agreeing with the
+//     round path to fp32 rounding.
+// Both leave split partials in one layout, merged by gqa_merge_kernel.
 //
-// Partial kernel, grid (max_splits, 2): block (s, g) owns one split of the
+// Round-path partial kernel, grid (max_splits, 2): block (s, g) owns one split of the
 // tokens of KV head g and serves all 8 query heads of the group, so every K/V
 // byte is read once.  A block is 8 waves = 32 groups of 16 lanes; lane li of a
 // group holds dims [8li, 8li+8) of all 8 query heads.  Split s owns tokens

@@ -13,6 +13,12 @@
  * textbook formulas with tolerances, the reference's own known-answer values
  * and smoke-test fixtures, closed forms and invariants.
  *
+ * Two GPU paths sum in an order this file does not restate, and are held to
+ * the mathematics instead (fp64 references with stated tolerances, closed
+ * forms): the multi-token prefill's MFMA GEMM and the matrix-core attention
+ * tactic of direct calls from 8192 cached tokens.  gqa() here restates the
+ * round path, which serves every other attention call.
+ *
  * Reference anchors (paths in lijeuki/KudaCuda):
  *   NF4 codebook / nibble order / dequant  kernels/common/nf4_device.cuh:10-40
  *   RMSNorm (fp32, x*inv_rms*gamma)        kernels/common/nf4_tiled_gemv.cuh:61-100,

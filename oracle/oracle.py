@@ -8,7 +8,9 @@ Thin numpy wrappers over ``liboracle.so`` (built from ``kc_oracle.c`` by
 ``build_oracle.sh``), whose functions restate the reference's decode math in
 the fixed fp32 operation order the kernels are specified to use, so results
 compare bit for bit.  Each wrapper names the reference code it follows; the
-restatement is pinned independently in ``tests/test_oracle_*.py``.
+restatement is pinned independently in ``tests/test_oracle_*.py``.  The
+prefill's MFMA GEMM and the matrix-core attention of long direct calls are
+not restated here; their GPU tests hold them to fp64 references instead.
 """
 
 from __future__ import annotations

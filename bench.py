@@ -142,11 +142,12 @@ def torch_cpu_per_config(threads: int) -> dict[tuple[str, int], dict]:
         return torch.randn(n, generator=gen) * std
 
     sample = "median of 20 calls after 3 warm-up, torch CPU fp32, weights dequantised once (excluded)"
+    cpu = _cpu_model()
     out: dict[tuple[str, int], dict] = {}
 
     def record(op: str, us: float, kv_len: int = 0) -> None:
-        out[(op, kv_len)] = {"value": round(us, 2), "unit": "us/call", "cores": threads, "kind": "port",
-                             "impl": "PyTorch eager (oracle/torch_cpu.py)", "sample": sample}
+        out[(op, kv_len)] = {"value": round(us, 2), "unit": "us/call", "cores": threads, "cpu": cpu,
+                             "kind": "port", "impl": "PyTorch eager (oracle/torch_cpu.py)", "sample": sample}
 
     w = nf4(2048, 2048)
     x = vec(2048)

@@ -5,9 +5,12 @@
 * registry_probe.hsaco: a gfx950 code object (`hipcc --genco`) that the
   registry loads at run time;
 * registry_smoke: a host program linked against kudacuda_amd/libkudacuda.so
-  (rpath relative to this folder) that drives include/kudacuda_registry.h.
+  (rpath relative to this folder) that drives include/kudacuda_registry.h;
+* split_plan_check: a host program over the split-KV plan helpers of
+  kudacuda_amd/csrc/kc_kernels.h.
 
-Both are built here on the CPU and run by tests/test_registry.py.
+All are built here on the CPU and run by tests/test_registry.py and
+tests/test_split_plan.py.
 """
 
 from __future__ import annotations
@@ -24,6 +27,7 @@ from kudacuda_amd import build as native_build  # noqa: E402
 
 PROBE = HERE / "registry_probe.hsaco"
 SMOKE = HERE / "registry_smoke"
+SPLIT_PLAN = HERE / "split_plan_check"
 
 
 def build() -> tuple[Path, Path]:
@@ -34,7 +38,10 @@ def build() -> tuple[Path, Path]:
     subprocess.run([hipcc, "-O2", "-std=c++17", "-Wall", str(HERE / "registry_smoke.cpp"), "-o", str(SMOKE),
                     f"-L{lib_dir}", "-lkudacuda", f"-Wl,-rpath,$ORIGIN/../../{lib_dir.name}"],
                    check=True, capture_output=True, text=True)
-    return PROBE, SMOKE
+    # host-only program over the split-plan helpers of kc_kernels.h
+    subprocess.run([hipcc, "-O2", "-std=c++17", "-Wall", str(HERE / "split_plan_check.cpp"), "-o", str(SPLIT_PLAN)],
+                   check=True, capture_output=True, text=True)
+    return PROBE, SMOKE, SPLIT_PLAN
 
 
 if __name__ == "__main__":

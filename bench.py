@@ -10,9 +10,15 @@ Timed region: K back-to-back replays of decode steps 63..63+K-1 (the steps
 that emit the 128 greedy tokens after the 64-token prompt), inputs resident in
 HBM, bracketed by stream synchronisation.  value = K / elapsed (tok/s).
 
-Also reported: per-kernel mean launch time from HIP events on the decode
+Also reported: the reference's per-token decode statistics (``reference_itl``:
+events around each token's step with a host sync per token, as
+tools/benchmark/benchmark_gemma.py:37-64,82-94 -- mean, median, p25, p75 ITL
+and 1000 / mean ITL) and the wall rate of that loop (``wall_host_sync``);
+per-kernel mean launch time from HIP events on the decode
 stream (each kernel launched back to back over all 36 layers, so weights are
-not cache resident), the roofline of the kernel that dominates the step, the
+not cache resident), the roofline of the kernel that dominates the step (its
+HIP-event time, or the committed rocprofv3 mean of profiles/roofline_rocprof.json
+when the two differ by more than 3 %, the other figure beside it), the
 multi-token prefill of the same 64-token prompt (kudacuda_qwen2_model_prefill,
 HIP events, median of 5) beside the 63 sequential decode steps the timed
 region starts after, and ``per_config``: BASELINE configs 1-4 (NF4 GEMV,
@@ -26,6 +32,7 @@ host; cpu_baseline_oracle times the C oracle (oracle/kc_oracle.c, OpenMP) the
 same way.
 
 Usage: python bench.py [--gpus 1] [--steps 128] [--warmup 16]
+       python bench.py --decode-only   (the run profiles/roofline_rocprof.json is traced from)
 """
 
 from __future__ import annotations
@@ -51,6 +58,8 @@ NEW_TOKENS = 128
 KV_BUCKET = 2048
 GOLDEN = ROOT / "tests" / "golden" / "decode_qwen25_3b_nf4.json"
 TRAFFIC = ROOT / "profiles" / "traffic.json"
+ROCPROF_MEANS = ROOT / "profiles" / "roofline_rocprof.json"
+AGREE = 0.03  # live HIP-event time and the committed rocprofv3 mean must agree this closely
 
 
 def measured_traffic(kernel: str) -> int | None:
@@ -61,6 +70,41 @@ def measured_traffic(kernel: str) -> int | None:
         return None
     entry = json.loads(TRAFFIC.read_text()).get("kernels", {}).get(kernel)
     return None if entry is None else int(entry["hbm_bytes"])
+
+
+def rocprof_mean(kernel: str) -> dict | None:
+    """The committed rocprofv3 kernel-trace mean duration of ``kernel`` in the
+    decode step (profiles/roofline_rocprof.json: the summary file and the
+    command that made it), or None if not profiled."""
+
+    if not ROCPROF_MEANS.exists():
+        return None
+    return json.loads(ROCPROF_MEANS.read_text()).get("kernels", {}).get(kernel)
+
+
+def roofline_entry(kernel: str, nbytes: int, event_ms: float) -> dict:
+    """Roofline of the dominant kernel.  ``achieved`` is its algorithmic bytes
+    over its mean launch time by HIP events, measured in this run, when that
+    time agrees with the committed rocprofv3 mean within AGREE; otherwise the
+    rocprofv3 mean is used and the HIP-event figure is reported beside it."""
+
+    live = nbytes / (event_ms * 1e-3) / 1e9
+    entry = {"kernel": kernel, "bound": "hbm", "achieved": round(live, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+             "frac": round(live / PEAK_HBM_GBS, 4), "traffic": measured_traffic(kernel), "bytes_per_launch": nbytes,
+             "time_source": "HIP events (this run)", "us_hip_events": round(event_ms * 1e3, 3)}
+    prof = rocprof_mean(kernel)
+    if prof is None:
+        return entry
+    prof_us = float(prof["mean_us"])
+    gap = event_ms * 1e3 / prof_us - 1.0
+    entry.update(us_rocprof=prof_us, rocprof_summary=prof["summary"], hip_events_vs_rocprof=round(gap, 4))
+    if abs(gap) > AGREE:
+        prof_gbs = nbytes / (prof_us * 1e-6) / 1e9
+        entry.update(achieved=round(prof_gbs, 1), frac=round(prof_gbs / PEAK_HBM_GBS, 4),
+                     time_source=f"rocprofv3 kernel-trace mean ({prof['summary']}): the HIP-event time of this run "
+                                 f"differs by {gap * 100:+.1f} %",
+                     achieved_hip_events=round(live, 1), frac_hip_events=round(live / PEAK_HBM_GBS, 4))
+    return entry
 
 
 # per-config case -> the kernels of profiles/traffic.json one launch runs
@@ -249,6 +293,9 @@ def main(argv: list[str] | None = None) -> int:
     parser.add_argument("--cpu-seconds", type=float, default=12.0)
     parser.add_argument("--op-iters", type=int, default=72)
     parser.add_argument("--no-per-config", action="store_true", help="skip BASELINE configs 1-4")
+    parser.add_argument("--decode-only", action="store_true",
+                        help="profiling run: the prompt, warm-up and timed decode steps and the per-kernel loop only "
+                             "(no per-token loop, prefill, per-config cases or CPU baselines)")
     args = parser.parse_args(argv)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -300,23 +347,45 @@ def main(argv: list[str] | None = None) -> int:
     print(f"[bench] {args.steps} steps in {elapsed * 1e3:.2f} ms (events {event_ms:.2f} ms)", file=sys.stderr,
           flush=True)
 
-    # Wall rate of a host loop that reads every token back before the next
-    # step (one synchronising round trip per token, as the reference's own
-    # loop pays for its host argmax); the metric above replays the steps back
-    # to back with the argmax and the token bookkeeping on the device.
-    model.set_step(PROMPT_LEN - 1)
-    stream.synchronize()
-    wall_tokens = []
-    t_wall = time.perf_counter()
-    for i in range(args.steps):
-        model.replay(1)
+    itl_report = wall_report = None
+    if not args.decode_only:
+        # The reference's own per-token protocol (tools/benchmark/benchmark_gemma.py:82-94,
+        # _timed_call): events around each token's step, then a host synchronisation
+        # and a host read of the token before the next step.  ITL statistics come from
+        # the events; the wall rate of the same loop includes the host round trip.
+        model.set_step(PROMPT_LEN - 1)
         stream.synchronize()
-        wall_tokens.append(int(model.tokens[PROMPT_LEN + i].item()))
-    wall_s = time.perf_counter() - t_wall
-    wall_report = {"tok_s": round(args.steps / wall_s, 1), "ms_per_token": round(wall_s * 1e3 / args.steps, 4),
-                   "tokens_equal": bool(np.array_equal(np.asarray(wall_tokens), tokens)),
-                   "what": "one graph replay, stream sync and host read of the token per step"}
-    print(f"[bench] host-synchronised loop: {wall_report['tok_s']} tok/s", file=sys.stderr, flush=True)
+        wall_tokens, itl_ms = [], []
+        t_wall = time.perf_counter()
+        for i in range(args.steps):
+            ev0 = torch.cuda.Event(enable_timing=True)
+            ev1 = torch.cuda.Event(enable_timing=True)
+            ev0.record(stream)
+            model.replay(1)
+            ev1.record(stream)
+            ev1.synchronize()
+            itl_ms.append(ev0.elapsed_time(ev1))
+            wall_tokens.append(int(model.tokens[PROMPT_LEN + i].item()))
+        wall_s = time.perf_counter() - t_wall
+        tokens_equal = bool(np.array_equal(np.asarray(wall_tokens), tokens))
+        wall_report = {"tok_s": round(args.steps / wall_s, 1), "ms_per_token": round(wall_s * 1e3 / args.steps, 4),
+                       "tokens_equal": tokens_equal,
+                       "what": "wall rate of a host loop that runs one graph replay per token between two events, "
+                               "synchronises and reads the token back before the next step (the reference's "
+                               "per-token loop, tools/benchmark/benchmark_gemma.py:82-94, host round trip included)"}
+        itl = np.asarray(itl_ms, dtype=np.float64)
+        itl_report = {
+            "itl_ms_mean": round(float(itl.mean()), 5), "itl_ms_median": round(float(np.median(itl)), 5),
+            "itl_ms_p25": round(float(np.percentile(itl, 25)), 5), "itl_ms_p75": round(float(np.percentile(itl, 75)), 5),
+            "itl_ms_min": round(float(itl.min()), 5), "itl_ms_max": round(float(itl.max()), 5),
+            "steady_state_tok_s": round(1000.0 / float(itl.mean()), 2), "tokens": args.steps,
+            "tokens_equal": tokens_equal,
+            "what": "reference-equivalent decode statistics: per-token HIP-event time of one step with a host sync "
+                    "per token (tools/benchmark/benchmark_gemma.py:37-64,82-94; steady_state_tok_s = 1000 / mean ITL, "
+                    "as the reference's summarize_generation)",
+        }
+        print(f"[bench] per-token ITL mean {itl_report['itl_ms_mean']} ms (median {itl_report['itl_ms_median']}), "
+              f"host-synchronised wall {wall_report['tok_s']} tok/s", file=sys.stderr, flush=True)
 
     parity = None
     if GOLDEN.exists() and args.seed == SEED and args.layers == 36:
@@ -324,28 +393,30 @@ def main(argv: list[str] | None = None) -> int:
         n = min(len(golden["tokens"]), args.steps)
         parity = bool(np.array_equal(tokens[:n], np.asarray(golden["tokens"][:n])))
 
-    # multi-token prefill of the same prompt (all layers at once, MFMA GEMMs)
-    # beside the 63 sequential decode steps the measurement above starts from
-    model.prefill(prompt)  # warm (workspace allocation, code paths)
-    stream.synchronize()
-    prefill_runs = []
-    for _ in range(5):
-        model.reset(prompt)
-        p_start = torch.cuda.Event(enable_timing=True)
-        p_stop = torch.cuda.Event(enable_timing=True)
-        p_start.record(stream)
-        model.prefill(prompt)
-        p_stop.record(stream)
-        p_stop.synchronize()
-        prefill_runs.append(p_start.elapsed_time(p_stop))
-    prefill_ms = float(np.median(prefill_runs))
-    first_token_agrees = bool(int(model.tokens[PROMPT_LEN].item()) == int(tokens[0]))
-    prefill_report = {
-        "tokens": PROMPT_LEN, "ms": round(prefill_ms, 4), "tok_s": round(PROMPT_LEN / (prefill_ms * 1e-3), 1),
-        "sequential_decode_ms": round((PROMPT_LEN - 1) * event_ms / args.steps, 4),
-        "first_token_equals_sequential": first_token_agrees,
-    }
-    print(f"[bench] prefill of {PROMPT_LEN} tokens: {prefill_ms:.3f} ms", file=sys.stderr, flush=True)
+    prefill_report = None
+    if not args.decode_only:
+        # multi-token prefill of the same prompt (all layers at once, MFMA GEMMs)
+        # beside the 63 sequential decode steps the measurement above starts from
+        model.prefill(prompt)  # warm (workspace allocation, code paths)
+        stream.synchronize()
+        prefill_runs = []
+        for _ in range(5):
+            model.reset(prompt)
+            p_start = torch.cuda.Event(enable_timing=True)
+            p_stop = torch.cuda.Event(enable_timing=True)
+            p_start.record(stream)
+            model.prefill(prompt)
+            p_stop.record(stream)
+            p_stop.synchronize()
+            prefill_runs.append(p_start.elapsed_time(p_stop))
+        prefill_ms = float(np.median(prefill_runs))
+        first_token_agrees = bool(int(model.tokens[PROMPT_LEN].item()) == int(tokens[0]))
+        prefill_report = {
+            "tokens": PROMPT_LEN, "ms": round(prefill_ms, 4), "tok_s": round(PROMPT_LEN / (prefill_ms * 1e-3), 1),
+            "sequential_decode_ms": round((PROMPT_LEN - 1) * event_ms / args.steps, 4),
+            "first_token_equals_sequential": first_token_agrees,
+        }
+        print(f"[bench] prefill of {PROMPT_LEN} tokens: {prefill_ms:.3f} ms", file=sys.stderr, flush=True)
 
     # per-kernel timing (HIP events on the decode stream, layers cycled)
     kv_len = PROMPT_LEN + args.steps // 2
@@ -360,7 +431,6 @@ def main(argv: list[str] | None = None) -> int:
     totals = {op: per_op[op] * launches[op] for op in per_op}
     dominant = max(totals, key=totals.get)
     nbytes = op_bytes(cfg, cfg.vocab, kv_len)
-    achieved = nbytes[dominant] / (per_op[dominant] * 1e-3) / 1e9
     op_report = {
         op: {"ms": round(per_op[op], 5), "bytes": nbytes[op],
              "gbs": round(nbytes[op] / (per_op[op] * 1e-3) / 1e9, 1), "launches_per_step": launches[op]}
@@ -388,23 +458,18 @@ def main(argv: list[str] | None = None) -> int:
             "vocab": cfg.vocab, "weights": "nf4 blocksize 64, fp32 absmax", "activations": "bf16",
             "prompt_len": PROMPT_LEN, "new_tokens": args.steps, "kv_bucket": KV_BUCKET, "seed": args.seed,
         },
-        "roofline": {
-            "kernel": dominant,
-            "bound": "hbm",
-            "achieved": round(achieved, 1),
-            "peak": PEAK_HBM_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": measured_traffic(dominant),
-        },
+        "roofline": roofline_entry(dominant, nbytes[dominant], per_op[dominant]),
         "step_hbm_gbs": round(step_bytes(cfg, cfg.vocab, kv_len) * value / 1e9, 1),
         "per_kernel": op_report,
         "prefill": prefill_report,
+        "reference_itl": itl_report,
         "wall_host_sync": wall_report,
         "token_parity_vs_oracle": parity,
         "reference_rtx3050_fp16_tok_s": 51.825,
     }
-    if not args.no_per_config:
+    if args.decode_only:
+        result["mode"] = "decode-only profiling run: not the benchmark line"
+    if not args.no_per_config and not args.decode_only:
         from kudacuda_amd import opbench
 
         print("[bench] BASELINE configs 1-4 on the GPU", file=sys.stderr, flush=True)
@@ -425,7 +490,7 @@ def main(argv: list[str] | None = None) -> int:
                 entry["speedup_vs_cpu"] = round(cpu["value"] / case["us"], 1)
             per_config.append(entry)
         result["per_config"] = per_config
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and not args.decode_only:
         print("[bench] timing the PyTorch-CPU decoder baseline", file=sys.stderr, flush=True)
         names = [f"{n}_{part}" for n in ("q", "k", "v", "o", "gate", "up", "down") for part in ("packed", "absmax")]
         host_layers = [{n: layer[n].cpu() for n in names} | {n: layer[n].view(torch.int16).cpu().numpy().view(np.uint16)

@@ -50,8 +50,14 @@ constexpr int kElfClass64 = 2;
 constexpr uint16_t kElfMachineAmdgpu = 224;  // EM_AMDGPU
 constexpr char kBundleMagic[] = "__CLANG_OFFLOAD_BUNDLE__";
 constexpr size_t kBundleMagicLen = sizeof(kBundleMagic) - 1;
+// `hipcc --genco --offload-compress` writes a compressed offload bundle: this
+// magic, then a version, the compression method and sizes, then the
+// compressed bundle.  Its entries cannot be read without decompressing, so
+// it is handed to hipModuleLoad, which decompresses it and judges the target.
+constexpr char kCompressedBundleMagic[] = "CCOB";
+constexpr size_t kCompressedBundleMagicLen = sizeof(kCompressedBundleMagic) - 1;
 
-enum class CodeObject { kUnreadable, kForeign, kAmdgpu };
+enum class CodeObject { kUnreadable, kForeign, kAmdgpu, kCompressedBundle };
 
 // ELF identification and e_machine of the 20 bytes at `p`.
 bool is_amdgpu_elf(const unsigned char* p, size_t n) {
@@ -72,7 +78,8 @@ uint64_t le64(const unsigned char* p) {
     return v;
 }
 
-// A code object as hipModuleLoad takes it: an AMDGPU ELF, or a clang offload
+// A code object as hipModuleLoad takes it: an AMDGPU ELF, a compressed
+// offload bundle (passed through, see above), or a clang offload
 // bundle (what `hipcc --genco` writes: magic, entry count, then per entry
 // offset, size, id length and id, all little-endian uint64) with an
 // "amdgcn-amd-amdhsa" entry whose payload is an AMDGPU ELF.
@@ -84,6 +91,10 @@ CodeObject inspect_code_object(const std::string& path) {
     std::vector<unsigned char> bytes((std::istreambuf_iterator<char>(file)), std::istreambuf_iterator<char>());
     if (is_amdgpu_elf(bytes.data(), bytes.size())) {
         return CodeObject::kAmdgpu;
+    }
+    if (bytes.size() >= kCompressedBundleMagicLen &&
+        std::memcmp(bytes.data(), kCompressedBundleMagic, kCompressedBundleMagicLen) == 0) {
+        return CodeObject::kCompressedBundle;
     }
     if (bytes.size() < kBundleMagicLen + 8 || std::memcmp(bytes.data(), kBundleMagic, kBundleMagicLen) != 0) {
         return CodeObject::kForeign;
@@ -142,6 +153,7 @@ int KudaCudaModuleRegistry::load(const std::string& name, const std::string& pat
         case CodeObject::kForeign:
             return outcome.refuse("not an AMDGPU code object (hipcc --genco): " + path);
         case CodeObject::kAmdgpu:
+        case CodeObject::kCompressedBundle:
             break;
     }
     if (const hipError_t status = hipSetDevice(device_id_); status != hipSuccess) {

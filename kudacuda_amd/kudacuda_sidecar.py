@@ -771,6 +771,9 @@ class KudaCudaBridge:
                 raise CacheCommittedError(f"KV cache update failed: {type(error).__name__}: {error}") from error
 
         route = self._attention_route(torch, call, query, key, value, graph_mode)
+        if route.startswith("decline:"):
+            self.last_qwen2_dispatch_reason = route[len("decline:"):]
+            return None
         if route == "native":
             try:
                 if graph_mode:
@@ -809,8 +812,10 @@ class KudaCudaBridge:
         mask = call.mask
         if mask is not None:
             if int(mask.shape[-1]) != kv_len:
-                raise CacheCommittedError(f"attention mask covers {int(mask.shape[-1])} keys but the cache holds "
-                                          f"{kv_len}")
+                reason = f"attention mask covers {int(mask.shape[-1])} keys but the cache holds {kv_len}"
+                if call.committed:
+                    raise CacheCommittedError(reason)
+                return f"decline:mask_length:{reason}"  # nothing written: the framework forward can run
             if not bool(torch.all(mask == 0)):
                 return "framework_fallback:attention_mask_values"
         if not (query.is_contiguous() and key.is_contiguous()):

@@ -109,10 +109,12 @@ def nf4_dequant_f64(packed: np.ndarray, absmax: np.ndarray, n: int, blocksize: i
 
 
 def rmsnorm_f64(x: np.ndarray, gamma: np.ndarray | None, eps: float) -> np.ndarray:
+    """Row-wise over the last axis (a 1-D vector is one row)."""
+
     x = x.astype(np.float64)
     if gamma is None:
         return x
-    return x / np.sqrt(np.mean(x * x) + eps) * gamma.astype(np.float64)
+    return x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps) * gamma.astype(np.float64)
 
 
 def silu_f64(g: np.ndarray) -> np.ndarray:

@@ -28,6 +28,7 @@ import pytest
 
 from kudacuda_amd import kudacuda_sidecar as S
 from kudacuda_amd import nf4_params as P
+from kudacuda_amd.kudacuda_graph_plan import GraphContractError
 from kudacuda_amd.kudacuda_static_decode import GraphStaticCache, StaticDecodeGraphRunner
 
 pytestmark = pytest.mark.gpu
@@ -239,3 +240,86 @@ def test_static_graph_runner_replays_decode_like_the_fp32_model(torch_gpu, bridg
         if runner_state is not None and runner_state.captured:
             runner_state.invalidate("test end")
         unpatch()
+
+
+def test_static_graph_runner_native_recorder_replays_decode_like_the_fp32_model(torch_gpu, bridge, models):
+    """The same runner with ``stream=None``: the forward is recorded by the
+    bridge's own hipGraph (kudacuda_begin_capture / end_capture on the
+    caller's stream, replayed by kudacuda_replay_graph), the path the
+    reference takes when PyTorch has no graph API
+    (python/kudacuda_static_decode.py:317-348).  PyTorch does not know about
+    this capture, so the forward's temporaries are allocated from a private
+    memory pool that is warmed by one eager forward first (no device
+    allocation inside the capture) and kept until the graph is reset: blocks
+    the replays write are never handed to other tensors."""
+
+    torch = torch_gpu
+    cpu, gpu, prompt = models
+    print("seam: StaticDecodeGraphRunner on the native recorder", flush=True)
+    unpatch = S.patch_qwen2_fused_qkv(gpu, bridge, tactic_name=QKV_TACTIC, attention_tactic_name=GQA_GRAPH_TACTIC)
+    runner = None
+    pool = torch.cuda.MemPool()
+    try:
+        want_tokens, want_logits = _greedy_eager(torch, gpu, prompt, NEW)
+        from transformers import DynamicCache
+
+        cache = DynamicCache(config=gpu.config)
+        with torch.inference_mode():
+            for pos in range(PROMPT):
+                _step(torch, gpu, prompt[pos], pos, cache)
+        torch.cuda.synchronize()
+        static = GraphStaticCache.from_dynamic_cache(torch, cache, max_cache_len=BUCKET)
+        stream = torch.cuda.Stream()
+        dev = "cuda:0"
+        mask = {"full_attention": torch.zeros((1, 1, 1, BUCKET), dtype=torch.bfloat16, device=dev)}
+        got = []
+        pos = PROMPT
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream), torch.cuda.use_mem_pool(pool):
+            # warm the pool: the capture's forward then finds every block it needs
+            kv_len_device = torch.tensor([pos + 1], dtype=torch.int32, device=dev)
+            static.cache_position.copy_(torch.tensor([pos], device=dev))
+            bridge.configure_qwen2_graph_dispatch(kv_len_device=kv_len_device, kv_capacity=BUCKET)
+            try:
+                with torch.inference_mode():
+                    gpu(input_ids=torch.tensor([[want_tokens[pos]]], device=dev),
+                        position_ids=torch.tensor([[pos]], device=dev), attention_mask=mask, past_key_values=static,
+                        cache_position=static.cache_position, use_cache=True, return_dict=True)
+            finally:
+                bridge.clear_qwen2_graph_dispatch()
+            stream.synchronize()
+            runner = StaticDecodeGraphRunner(bridge, gpu, torch)
+            runner.capture(input_ids=torch.tensor([[want_tokens[pos]]], device=dev),
+                           position_ids=torch.tensor([[pos]], device=dev), attention_mask=mask,
+                           cache_position=static.cache_position, past_key_values=static, logical_kv_len=pos,
+                           kv_bucket=BUCKET, tactic_name=GQA_GRAPH_TACTIC, stream_ptr=int(stream.cuda_stream),
+                           stream=None)
+        assert runner.backend == "native" and runner.cuda_graph is None
+        with torch.cuda.stream(stream):
+            stream.synchronize()
+            assert bridge.last_qwen2_dispatch_reason == "native", bridge.last_qwen2_dispatch_reason
+            got.append(runner.logits[0, -1].float().cpu())
+            for pos in range(PROMPT + 1, PROMPT + NEW - 1):
+                runner.replay(next_token=torch.tensor([[want_tokens[pos]]], device=dev),
+                              position_ids=torch.tensor([[pos]], device=dev), cache_position=pos,
+                              logical_kv_len=pos, stream_ptr=int(stream.cuda_stream))
+                stream.synchronize()
+                got.append(runner.logits[0, -1].float().cpu())
+        torch.cuda.synchronize()
+        assert runner.replay_count == NEW - 1
+        got = torch.stack(got)
+        ref = want_logits[1: 1 + got.shape[0]]
+        err = (got - ref).abs().max().item()
+        print(f"native graph replay vs eager max |diff| {err:.3g} over {got.shape[0]} steps", flush=True)
+        assert err <= LOGIT_ATOL
+        _check_against_cpu(torch, cpu, want_tokens[: PROMPT + NEW - 1], torch.cat([want_logits[:1], got]))
+        # a replay whose stream differs from the captured one is refused before anything runs
+        with pytest.raises(GraphContractError, match="stream changed"):
+            runner.replay(next_token=torch.tensor([[0]], device=dev), position_ids=torch.tensor([[pos]], device=dev),
+                          cache_position=pos, logical_kv_len=pos, stream_ptr=int(stream.cuda_stream) + 1)
+    finally:
+        torch.cuda.synchronize()
+        if runner is not None and runner.captured:
+            runner.invalidate("test end")
+        unpatch()
+        del runner

@@ -14,11 +14,12 @@ import pytest
 HERE = Path(__file__).resolve().parent
 SMOKE = HERE / "native" / "registry_smoke"
 PROBE = HERE / "native" / "registry_probe.hsaco"
+PROBE_COMPRESSED = HERE / "native" / "registry_probe_ccob.hsaco"
 LIB = HERE.parent / "kudacuda_amd" / "libkudacuda.so"
 
 
 def _built() -> None:
-    if not (SMOKE.exists() and PROBE.exists()):
+    if not (SMOKE.exists() and PROBE.exists() and PROBE_COMPRESSED.exists()):
         pytest.skip("native smokes not built (python tests/native/build.py)")
 
 
@@ -40,10 +41,20 @@ def test_registry_without_a_device_refuses_every_call():
     assert "registry smoke ok (no device)" in run.stdout
 
 
-@pytest.mark.gpu
-def test_registry_loads_resolves_launches_and_freezes():
+def test_compressed_probe_is_a_compressed_offload_bundle():
+    """The second probe starts with the compressed-bundle magic the registry
+    passes through to hipModuleLoad (and is smaller than the plain one)."""
+
     _built()
-    print(f"registry smoke: {SMOKE} {PROBE}", flush=True)
-    run = subprocess.run([str(SMOKE), str(PROBE)], capture_output=True, text=True, timeout=120)
+    assert PROBE_COMPRESSED.read_bytes()[:4] == b"CCOB"
+    assert PROBE.read_bytes()[:4] != b"CCOB"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("probe", [PROBE, PROBE_COMPRESSED], ids=["plain", "compressed"])
+def test_registry_loads_resolves_launches_and_freezes(probe):
+    _built()
+    print(f"registry smoke: {SMOKE} {probe}", flush=True)
+    run = subprocess.run([str(SMOKE), str(probe)], capture_output=True, text=True, timeout=120)
     assert run.returncode == 0, run.stdout + run.stderr
     assert "registry smoke ok (1000 outputs via probe_affine)" in run.stdout

@@ -120,3 +120,22 @@ def test_mask_disagreeing_with_the_cache_raises_instead_of_rerunning(setup):
         with torch.no_grad():
             s["module"](hidden, emb, mask, past_key_values=s["patched"], cache_position=cache_pos)
     assert s["patched"].get_seq_length(0) == before + 1
+
+
+def test_mask_disagreeing_without_a_cache_declines_to_the_framework(setup):
+    """Without a cache nothing is written before the route is chosen, so a
+    mask of another key count is a plain decline: the guard returns None and
+    the framework forward runs on the same arguments -- here the framework
+    rejects the mask itself, with its own error and not CacheCommittedError."""
+
+    s = setup
+    hidden, emb, cache_pos = _decode_inputs(s, 0)
+    mask = torch.zeros(1, 1, 1, 5)  # one token attends to itself; the mask is longer
+    with torch.no_grad():
+        with pytest.raises(RuntimeError) as framework:
+            s["original"](s["module"], hidden, emb, mask, past_key_values=None, cache_position=cache_pos)
+        with pytest.raises(RuntimeError) as patched:
+            s["module"](hidden, emb, mask, past_key_values=None, cache_position=cache_pos)
+    assert not isinstance(patched.value, S.CacheCommittedError)
+    assert str(patched.value) == str(framework.value)
+    assert s["bridge"].last_qwen2_dispatch_reason.startswith("mask_length:"), s["bridge"].last_qwen2_dispatch_reason

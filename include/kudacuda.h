@@ -242,9 +242,9 @@ KUDACUDA_API int kudacuda_qwen2_gqa_decode_graph_bf16(void* handle, uint64_t que
  * results) for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Its
  * split partials and ticket counters live in a fixed static device array of
- * the library (~4.3 MB per GPU, held until the process ends) instead of the
- * handle's scratch; the call itself allocates nothing.  kv_capacity 1..32768
- * (larger is rejected with status 1).  Every call on one GPU shares that
+ * the library (2,130,176 B per GPU, held until the process ends) instead of
+ * the handle's scratch; the call itself allocates nothing.  kv_capacity
+ * 1..65536, as for the allocating twin (larger is rejected with status 1).  Every call on one GPU shares that
  * array, so calls that overlap on one GPU (two streams, two handles) race;
  * serialise them. */
 KUDACUDA_API int kudacuda_qwen2_gqa_decode_graph_bf16_noalloc(void* handle, uint64_t query, uint64_t key_cache,

@@ -41,8 +41,11 @@ constexpr int64_t kMaxModelKv = 32768;
 // Host code never passes `scratch` itself to a kernel: its name is a host-side
 // stand-in, so every use goes through the device address that
 // hipGetSymbolAddress returned on that device (static_scratch_on()).
-constexpr int64_t kNoAllocMaxKv = 32768;
-constexpr int64_t kNoAllocMaxSplits = 512;
+// Capacity up to the allocating twin's 65536 tokens: every graph-mode plan
+// (split cap kGqaSplitCap per KV head, whatever the capacity) fits.
+constexpr int64_t kNoAllocMaxKv = kMaxStandaloneKv;
+constexpr int64_t kNoAllocMaxSplits = kGqaSplitCap;
+static_assert(kNoAllocMaxSplits >= kGqaSplitCap, "the static partials hold the largest graph-mode split plan");
 constexpr int64_t kNoAllocCounterBytes = 256;
 constexpr int64_t kNoAllocPartialFloats = 16 * kNoAllocMaxSplits * kGqaPartialStride;
 constexpr int64_t kNoAllocScratchBytes = kNoAllocCounterBytes + kNoAllocPartialFloats * 4;

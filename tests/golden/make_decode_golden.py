@@ -6,8 +6,11 @@ Fixture = the seeded synthetic Qwen2.5-3B-shaped NF4 model (
 variant small enough for the CPU test suite.  Stored: prompt, generated ids,
 the bf16 top-1 minus top-2 logit margin at each generated token, SHA-256
 digests of the bf16 logits and of the final hidden state (the residual stream
-after the last layer) after every step that emits a token, and SHA-256
-digests of the oracle-quantised layer-0 weights.
+after the last layer) after every step that emits a token, SHA-256 digests
+of every layer's key and value cache rows of the prompt tokens (rows
+0..prompt_len-1 of [2, capacity, 128] bf16, written by the prompt steps and
+never changed after), and SHA-256 digests of the oracle-quantised layer-0
+weights.
 
 Usage: python tests/golden/make_decode_golden.py [--small-only]
 """
@@ -54,10 +57,16 @@ def run(name: str, *, num_layers: int, vocab: int, kv_capacity: int, prompt_len:
         f"layer0_{n}": hashlib.sha256(model.layers[0][n].tobytes()).hexdigest()
         for n in ("q_packed", "q_absmax", "down_packed", "down_absmax")
     }
+    prompt_kv = [
+        {"key": hashlib.sha256(np.ascontiguousarray(layer["key_cache"][:, :prompt_len]).tobytes()).hexdigest(),
+         "value": hashlib.sha256(np.ascontiguousarray(layer["value_cache"][:, :prompt_len]).tobytes()).hexdigest()}
+        for layer in model.layers
+    ]
     payload = {
         "seed": SEED, "num_layers": num_layers, "vocab": vocab, "kv_capacity": kv_capacity,
         "prompt": prompt.astype(int).tolist(), "tokens": tokens, "logit_margins": margins,
-        "logits_sha256": logit_digests, "hidden_sha256": hidden_digests, "weight_digests": digests, "generator": "tests/golden/make_decode_golden.py (oracle/kc_oracle.c)",
+        "logits_sha256": logit_digests, "hidden_sha256": hidden_digests, "weight_digests": digests,
+        "prompt_kv_sha256": prompt_kv, "generator": "tests/golden/make_decode_golden.py (oracle/kc_oracle.c)",
     }
     (OUT / f"{name}.json").write_text(json.dumps(payload, indent=1) + "\n", encoding="utf-8")
     print(f"{name}: build {t1 - t0:.1f}s decode {time.time() - t1:.1f}s tokens {tokens[:16]}... "

@@ -2,6 +2,7 @@
 
 from __future__ import annotations
 
+import hashlib
 import json
 import math
 from pathlib import Path
@@ -118,6 +119,10 @@ def test_oracle_reproduces_the_small_golden_fixture():
     assert prompt.tolist() == synthetic.prompt_ids(golden["seed"], prompt.size, golden["vocab"]).tolist()
     out = hm.generate(prompt, len(golden["tokens"]))
     assert out.tolist() == golden["tokens"]
+    for layer, want in zip(hm.layers, golden["prompt_kv_sha256"]):
+        for name, key in (("key_cache", "key"), ("value_cache", "value")):
+            rows = np.ascontiguousarray(layer[name][:, : prompt.size])
+            assert hashlib.sha256(rows.tobytes()).hexdigest() == want[key]
 
 
 def test_stop_token_ends_the_decode_and_freezes_the_state():

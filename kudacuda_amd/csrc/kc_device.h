@@ -231,25 +231,30 @@ __device__ __forceinline__ uint32_t take_ticket(uint32_t* counter) {
 __device__ __forceinline__ void wait_own_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // ------------------------------------------------------------------ NF4 dots
-// (byte B of x) << 3 in one instruction (a byte-select shift), written as
+// (byte B of x) << S in one instruction (a byte-select shift), written as
 // asm: the compiler folds a byte-select operand back into a shift and an AND.
-template <int B>
-__device__ __forceinline__ uint32_t byte_shl3(uint32_t x) {
+template <int B, int S>
+__device__ __forceinline__ uint32_t byte_shl(uint32_t x) {
     uint32_t r;
     if constexpr (B == 0) {
         asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
-            : "=v"(r) : "v"(3u), "v"(x));
+            : "=v"(r) : "v"(static_cast<uint32_t>(S)), "v"(x));
     } else if constexpr (B == 1) {
         asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1"
-            : "=v"(r) : "v"(3u), "v"(x));
+            : "=v"(r) : "v"(static_cast<uint32_t>(S)), "v"(x));
     } else if constexpr (B == 2) {
         asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2"
-            : "=v"(r) : "v"(3u), "v"(x));
+            : "=v"(r) : "v"(static_cast<uint32_t>(S)), "v"(x));
     } else {
         asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3"
-            : "=v"(r) : "v"(3u), "v"(x));
+            : "=v"(r) : "v"(static_cast<uint32_t>(S)), "v"(x));
     }
     return r;
+}
+
+template <int B>
+__device__ __forceinline__ uint32_t byte_shl3(uint32_t x) {
+    return byte_shl<B, 3>(x);
 }
 
 // Where a lane finds byte value e's entry of the pair table in LDS: the
@@ -270,6 +275,20 @@ struct SlicedLookup {
     template <int B>
     __device__ __forceinline__ const float2* entry(uint32_t w) const {
         return reinterpret_cast<const float2*>(base + __builtin_amdgcn_perm(w, slot8, 0x0c0c0400u | (B << 8)));
+    }
+};
+
+// ... or a compact copy of 16 interleaved tables (see copy16_entry_store):
+// copy c of entry e at byte e * 128 + 8 c, lane l reading copy l % 16 --
+// one byte-select shift and one OR.  The 32 lanes of an 8-byte LDS pass use
+// 16 bank pairs twice; lanes l and l + 16 collide only when their entries
+// have the same parity.  32 KiB, for kernels that cannot spend 64 KiB.
+struct Copy16Lookup {
+    const char* base;
+    uint32_t copy8;
+    template <int B>
+    __device__ __forceinline__ const float2* entry(uint32_t w) const {
+        return reinterpret_cast<const float2*>(base + (byte_shl<B, 7>(w) | copy8));
     }
 };
 
@@ -430,6 +449,22 @@ __device__ __forceinline__ void sliced_entry_store(float* sliced, float2 e) {
             row[(j + threadIdx.x) & (kNf4Slots - 1)] = e;
         }
     }
+}
+constexpr int kNf4Copies16 = 16;
+constexpr int kNf4Copy16Floats = 2 * kNf4PairEntries * kNf4Copies16;
+// Thread t < 256 writes its entry (pair_entry_fetch) into the 16 copies,
+// copy (j + t) % 16 at step j; the caller publishes with a block barrier.
+__device__ __forceinline__ void copy16_entry_store(float* table, float2 e) {
+    if (threadIdx.x < kNf4PairEntries) {
+        float2* row = reinterpret_cast<float2*>(table) + threadIdx.x * kNf4Copies16;
+#pragma unroll
+        for (int j = 0; j < kNf4Copies16; ++j) {
+            row[(j + threadIdx.x) & (kNf4Copies16 - 1)] = e;
+        }
+    }
+}
+__device__ __forceinline__ Copy16Lookup copy16_lookup(const float* table) {
+    return Copy16Lookup{reinterpret_cast<const char*>(table), (threadIdx.x & (kNf4Copies16 - 1)) * 8u};
 }
 __device__ __forceinline__ SlicedLookup sliced_lookup(const float* sliced) {
     return SlicedLookup{reinterpret_cast<const char*>(sliced), (threadIdx.x & (kNf4Slots - 1)) * 8u};

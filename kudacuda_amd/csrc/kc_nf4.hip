@@ -285,7 +285,7 @@ __global__ __launch_bounds__(NTH) void nf4_rows2048_kernel(const void* h0, const
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t waves_per_block = NTH / 64;
     const int64_t nwaves = static_cast<int64_t>(gridDim.x) * waves_per_block;
-    const int64_t first = static_cast<int64_t>(blockIdx.x) * waves_per_block + wave;
+    const int64_t first = static_cast<int64_t>(xcd_contiguous(blockIdx.x, gridDim.x)) * waves_per_block + wave;
     static_assert(NTH >= kNf4PairEntries, "one pair-table entry per thread");
     const float2 pair_entry = pair_entry_fetch();
 
@@ -608,7 +608,7 @@ __global__ __launch_bounds__(64 * ((NCHUNK + 63) / 64)) void nf4_down_kernel(con
     const int cc = valid ? c : NCHUNK - 1;
     const int64_t row_chunks = NCHUNK;
     const int64_t row_blocks = NCHUNK / 2;
-    const int64_t rbase = static_cast<int64_t>(blockIdx.x) * R;
+    const int64_t rbase = static_cast<int64_t>(xcd_contiguous(blockIdx.x, gridDim.x)) * R;  // XCD-contiguous rows
     const int64_t last_row = a.rows - 1;
     static_assert(64 * W >= kNf4PairEntries, "one pair-table entry per thread");
     const float2 pair_entry = pair_entry_fetch();

@@ -6,12 +6,16 @@
 // python/kudacuda_sidecar.py:1719-1738, kernels/common/nf4_device.cuh:10-40)
 // and fp32 accumulation in v_mfma_f32_16x16x32_bf16.
 //
-// Tiling: a block is 4 waves and each wave owns one 16-row weight fragment
-// and all m <= 64 tokens (NT token tiles of 16, a template parameter so the
-// window loop is straight-line code).  kBias / kResidual: the block's waves
-// own output rows [n0, n0 + 64).  kSwiGlu: waves 0 and 1 own gate rows
-// [n0, n0 + 32), waves 2 and 3 the same up rows; the up sums reach the gate
-// waves through LDS for the epilogue.
+// Tiling: each wave owns one 16-row weight fragment and all m <= 64 tokens
+// (NT token tiles of 16, a template parameter so the window loop is
+// straight-line code).  kBias / kResidual / kQkvRope / kResidualNorm: blocks
+// of 4 waves own output rows [n0, n0 + 64).  kSwiGlu: blocks of 6 waves,
+// waves 0..2 own gate rows [n0, n0 + 48) and waves 3..5 the same up rows; the
+// up sums reach the gate waves through LDS for the epilogue.  A block's time
+// is set by its CU's LDS and VALU work, so the 11008-row gate/up launch is
+// one 6-wave block per CU (230 blocks; 4-wave blocks made 344, and the CUs
+// that ran two of them set the launch's length: 64-token prefill
+// 2.78 -> 2.72 ms).
 //
 // Operand layouts of the 16x16x32 bf16 MFMA (lane l, row l%16, group
 // q = l/16): A[l%16][8q + j], B[8q + j][l%16], D[4q + i][l%16].  With
@@ -52,29 +56,6 @@ constexpr int kWindow = 128;
 constexpr int kXPitch = kWindow * 2 + 16;  // bytes per staged token row
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
-
-// 8 codes of one 32-bit word (byte b: element 2b in the high nibble, 2b+1 in
-// the low nibble) times absmax, each rounded to bf16 (round to nearest even,
-// v_cvt_pk_bf16_f32; the products are finite); element j lands in slot j.
-// Both codes of byte b come from one 8-byte read of the LDS pair table, in
-// the block's 16-copy layout (Copy16Lookup: the lane's copy of entry b; its
-// bank conflicts are about a quarter of the single table's -- 64-token
-// prefill 2.90 -> 2.85 ms, bit-identical).
-template <int B>
-__device__ __forceinline__ void dequant_byte(bf16x8& v, uint32_t word, float am, const Copy16Lookup& lut) {
-    const float2 p = *lut.template entry<B>(word);
-    v[2 * B] = static_cast<__bf16>(p.x * am);
-    v[2 * B + 1] = static_cast<__bf16>(p.y * am);
-}
-
-__device__ __forceinline__ bf16x8 dequant8_bf16(uint32_t word, float am, const Copy16Lookup& lut) {
-    bf16x8 v;
-    dequant_byte<0>(v, word, am, lut);
-    dequant_byte<1>(v, word, am, lut);
-    dequant_byte<2>(v, word, am, lut);
-    dequant_byte<3>(v, word, am, lut);
-    return v;
-}
 
 // One window's x requests of a thread, kept as one vector value (slots
 // 4j..4j+3: its 16-byte piece of token row 16j + tid/16, bytes 16 (tid%16)
@@ -119,33 +100,78 @@ __device__ __forceinline__ void x_stage(uint8_t* buf, const u32x16& o, int tid) 
     }
 }
 
+// 8 codes of one 32-bit word (byte b: element 2b in the high nibble, 2b+1 in
+// the low nibble) times absmax, each rounded to bf16 (round to nearest even,
+// v_cvt_pk_bf16_f32; the products are finite); element j lands in slot j.
+// lookup4 makes the table reads, scale8_bf16 the products.
+// Both codes of byte b come from one 8-byte read of the LDS pair table, in
+// the block's 16-copy layout (Copy16Lookup: the lane's copy of entry b; its
+// bank conflicts are about a quarter of the single table's -- 64-token
+// prefill 2.90 -> 2.85 ms, bit-identical).
+__device__ __forceinline__ void lookup4(float2* p, uint32_t word, const Copy16Lookup& cb) {
+    p[0] = *cb.template entry<0>(word);
+    p[1] = *cb.template entry<1>(word);
+    p[2] = *cb.template entry<2>(word);
+    p[3] = *cb.template entry<3>(word);
+}
+
+__device__ __forceinline__ bf16x8 scale8_bf16(const float2* p, float am) {
+    bf16x8 v;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        v[2 * b] = static_cast<__bf16>(p[b].x * am);
+        v[2 * b + 1] = static_cast<__bf16>(p[b].y * am);
+    }
+    return v;
+}
+
+// One window: every LDS read of the window (16 table reads, 4 NT operand
+// tiles) is issued before the first is used, so the wave waits about one
+// LDS round trip per window; reads issued and consumed a few at a time
+// left the window a chain of ~25 dependent round trips.
 template <int NT>
 __device__ __forceinline__ void gemm_window(const uint8_t* buf, const u32x8& o, floatx4* acc, int r, int q,
                                             const Copy16Lookup& cb) {
     const float am = __uint_as_float(o[4]);
+    float2 p[4][4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-        const bf16x8 A = dequant8_bf16(o[s], am, cb);
+        lookup4(p[s], o[s], cb);
+    }
+    uint4 B[4][NT];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const uint4 B = *reinterpret_cast<const uint4*>(buf + (16 * t + r) * kXPitch + 64 * q + 16 * s);
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, as_bf16x8(B), acc[t], 0, 0, 0);
+            B[s][t] = *reinterpret_cast<const uint4*>(buf + (16 * t + r) * kXPitch + 64 * q + 16 * s);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const bf16x8 A = scale8_bf16(p[s], am);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, as_bf16x8(B[s][t]), acc[t], 0, 0, 0);
         }
     }
 }
 
-template <GemmEpi EPI, int NT>
-__global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(Nf4GemmArgs a) {
+template <GemmEpi EPI, int NT, int W = kGemmWaves>
+__global__ __launch_bounds__(64 * W) void nf4_gemm_kernel(Nf4GemmArgs a) {
     constexpr bool kSw = EPI == GemmEpi::kSwiGlu;
-    constexpr int kBlockRows = kSw ? kRowsPerBlock / 2 : kRowsPerBlock;  // output rows of the block
+    static_assert(!kSw || W % 2 == 0, "gate and up waves in pairs");
+    constexpr int kFrags = kSw ? W / 2 : W;                  // row fragments of the block per weight
+    constexpr int kBlockRows = kFrags * kRowsPerWave;        // output rows of the block
     __shared__ __attribute__((aligned(16))) float s_cb[kNf4Copy16Floats];
     __shared__ __attribute__((aligned(16))) uint8_t s_x[2][16 * NT * kXPitch];
     const Copy16Lookup cb = copy16_lookup(s_cb);
-    static_assert(kGemmThreads >= kNf4PairEntries, "one pair-table entry per thread");
+    static_assert(64 * W >= kNf4PairEntries, "one pair-table entry per thread");
     const float2 pair_entry = pair_entry_fetch();  // first request: its wait below waits for nothing else
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tx = tid & 255;  // x staging: threads 256.. repeat the first 256 (same data, same place)
     const int r = lane & 15;
     const int q = lane >> 4;
     const int64_t K = a.k;
@@ -157,11 +183,15 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(Nf4GemmArgs a) {
     const int64_t k_end = k_begin + per_split * kWindow < K ? k_begin + per_split * kWindow : K;
     // this wave's fragment: f = 0 (gate or plain) / 1 (up), first output
     // column n0w; kQkvRope: the block's 64 rows lie in the q, k or v weight
-    // (segment boundaries are multiples of 64), row0 is the row in it
-    const int f = kSw ? wave >> 1 : 0;
-    const int64_t n0w = static_cast<int64_t>(blockIdx.x) * kBlockRows + (kSw ? wave & 1 : wave) * kRowsPerWave;
+    // (segment boundaries are multiples of 64), row0 is the row in it.  A
+    // fragment past the last row (the last block of a 48-row gate/up split)
+    // computes the last fragment again and stores nothing.
+    const int f = kSw ? wave / kFrags : 0;
+    const int frag = kSw ? wave % kFrags : wave;
+    const int64_t n0w = static_cast<int64_t>(blockIdx.x) * kBlockRows + frag * kRowsPerWave;
+    const bool live = n0w < a.n;
     int seg = f;
-    int64_t row0 = n0w;
+    int64_t row0 = live ? n0w : a.n - kRowsPerWave;
     if constexpr (EPI == GemmEpi::kQkvRope) {
         seg = n0w < a.q_rows ? 0 : (n0w < a.q_rows + a.kv_rows ? 1 : 2);
         row0 = n0w - (seg == 0 ? 0 : (seg == 1 ? a.q_rows : a.q_rows + a.kv_rows));
@@ -172,10 +202,10 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(Nf4GemmArgs a) {
     const uint16_t* xrow[NT];
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
-        const int m = 16 * j + tid / 16 < M ? 16 * j + tid / 16 : M - 1;
+        const int m = 16 * j + tx / 16 < M ? 16 * j + tx / 16 : M - 1;
         xrow[j] = a.x + static_cast<int64_t>(m) * K;
     }
-    const int xcol = 8 * (tid % 16);
+    const int xcol = 8 * (tx % 16);
 
     floatx4 acc[NT];
 #pragma unroll
@@ -196,7 +226,7 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(Nf4GemmArgs a) {
     u32x8 w1 = w_fetch(wrow, arow, k1, q);
     u32x16 x2;
     u32x8 w2;
-    x_stage<NT>(sx, x0, tid);
+    x_stage<NT>(sx, x0, tx);
     copy16_entry_store(s_cb, pair_entry);
     __syncthreads();
     int buf = 0;
@@ -208,7 +238,7 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(Nf4GemmArgs a) {
         WF = w_fetch(wrow, arow, kf, q);                                           \
         __builtin_amdgcn_sched_barrier(0); /* requests ahead of the compute */     \
         gemm_window<NT>(sx + buf * kBuf, WC, acc, r, q, cb);                      \
-        x_stage<NT>(sx + (buf ^ 1) * kBuf, XS, tid);                               \
+        x_stage<NT>(sx + (buf ^ 1) * kBuf, XS, tx);                                \
         __syncthreads();                                                           \
         buf ^= 1;                                                                  \
         kw += kWindow;                                                             \
@@ -229,7 +259,7 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(Nf4GemmArgs a) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const int m = 16 * t + r;
-            if (m < M) {
+            if (m < M && live) {
                 float* dst = a.partials + ((static_cast<int64_t>(f) * S + blockIdx.y) * M + m) * a.n + n0w + 4 * q;
                 *reinterpret_cast<float4*>(dst) = make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
             }
@@ -247,7 +277,7 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(Nf4GemmArgs a) {
         if (f == 1) {
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                s_up[((wave & 1) * NT + t) * 64 + lane] = acc[t];
+                s_up[(frag * NT + t) * 64 + lane] = acc[t];
             }
         }
         __syncthreads();
@@ -256,13 +286,13 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(Nf4GemmArgs a) {
         }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            up[t] = s_up[((wave & 1) * NT + t) * 64 + lane];
+            up[t] = s_up[(frag * NT + t) * 64 + lane];
         }
     }
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         const int m = 16 * t + r;
-        if (m >= M) {
+        if (m >= M || !live) {
             continue;
         }
         const int64_t nb = n0w + 4 * q;
@@ -501,21 +531,43 @@ hipError_t launch_gemm_epi(const Nf4GemmArgs& a, hipStream_t stream) {
             S = (windows + per_split - 1) / per_split;  // no empty split
         }
     }
-    const int64_t block_rows = EPI == GemmEpi::kSwiGlu ? kRowsPerBlock / 2 : kRowsPerBlock;
-    const dim3 grid(static_cast<unsigned>(a.n / block_rows), static_cast<unsigned>(S));
-    switch ((a.m + 15) / 16) {
-        case 1:
-            hipLaunchKernelGGL((nf4_gemm_kernel<EPI, 1>), grid, dim3(kGemmThreads), 0, stream, a);
-            break;
-        case 2:
-            hipLaunchKernelGGL((nf4_gemm_kernel<EPI, 2>), grid, dim3(kGemmThreads), 0, stream, a);
-            break;
-        case 3:
-            hipLaunchKernelGGL((nf4_gemm_kernel<EPI, 3>), grid, dim3(kGemmThreads), 0, stream, a);
-            break;
-        default:
-            hipLaunchKernelGGL((nf4_gemm_kernel<EPI, kTokenTiles>), grid, dim3(kGemmThreads), 0, stream, a);
-            break;
+    if constexpr (EPI == GemmEpi::kSwiGlu) {
+        // 6-wave blocks of 48 gate + 48 up rows: 11008 rows make 230 blocks,
+        // one per CU (4-wave blocks made 344, so a third of the CUs ran two)
+        constexpr int kSwWaves = 6;
+        constexpr int64_t kSwRows = kSwWaves / 2 * kRowsPerWave;
+        const dim3 grid(static_cast<unsigned>((a.n + kSwRows - 1) / kSwRows), static_cast<unsigned>(S));
+        const dim3 block(64 * kSwWaves);
+        switch ((a.m + 15) / 16) {
+            case 1:
+                hipLaunchKernelGGL((nf4_gemm_kernel<EPI, 1, kSwWaves>), grid, block, 0, stream, a);
+                break;
+            case 2:
+                hipLaunchKernelGGL((nf4_gemm_kernel<EPI, 2, kSwWaves>), grid, block, 0, stream, a);
+                break;
+            case 3:
+                hipLaunchKernelGGL((nf4_gemm_kernel<EPI, 3, kSwWaves>), grid, block, 0, stream, a);
+                break;
+            default:
+                hipLaunchKernelGGL((nf4_gemm_kernel<EPI, kTokenTiles, kSwWaves>), grid, block, 0, stream, a);
+                break;
+        }
+    } else {
+        const dim3 grid(static_cast<unsigned>(a.n / kRowsPerBlock), static_cast<unsigned>(S));
+        switch ((a.m + 15) / 16) {
+            case 1:
+                hipLaunchKernelGGL((nf4_gemm_kernel<EPI, 1>), grid, dim3(kGemmThreads), 0, stream, a);
+                break;
+            case 2:
+                hipLaunchKernelGGL((nf4_gemm_kernel<EPI, 2>), grid, dim3(kGemmThreads), 0, stream, a);
+                break;
+            case 3:
+                hipLaunchKernelGGL((nf4_gemm_kernel<EPI, 3>), grid, dim3(kGemmThreads), 0, stream, a);
+                break;
+            default:
+                hipLaunchKernelGGL((nf4_gemm_kernel<EPI, kTokenTiles>), grid, dim3(kGemmThreads), 0, stream, a);
+                break;
+        }
     }
     hipError_t status = hipGetLastError();
     if (status != hipSuccess || S == 1) {

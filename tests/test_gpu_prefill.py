@@ -76,12 +76,15 @@ def test_nf4_gemm_matches_fp64(torch_gpu, native, stream, m, n, k, epi):
     _close(host(out).reshape(m, n), want, inner=acc if epi == "residual" else None)
 
 
-@pytest.mark.parametrize("m", [1, 13, 64])
-def test_nf4_gemm_swiglu_matches_fp64(torch_gpu, native, stream, m):
+# Gate/up blocks hold 48 rows of each weight: 11008 rows leave the last
+# block one live 16-row fragment of three, 128 rows two, 192 none dead (the
+# small widths also take the split-K path).
+@pytest.mark.parametrize("m,n", [(1, 11008), (13, 11008), (64, 11008), (64, 128), (5, 192)])
+def test_nf4_gemm_swiglu_matches_fp64(torch_gpu, native, stream, m, n):
     torch = torch_gpu
-    n, k = 11008, 2048
-    rng = np.random.default_rng([SEED, 7, m])
-    print(f"nf4_gemm_swiglu m={m}", flush=True)
+    k = 2048
+    rng = np.random.default_rng([SEED, 7, m] if n == 11008 else [SEED, 7, m, n])
+    print(f"nf4_gemm_swiglu m={m} n={n}", flush=True)
     gp, ga, gw = _weights(rng, n, k)
     up, ua, uw = _weights(rng, n, k)
     xb, x = _acts(rng, m, k)

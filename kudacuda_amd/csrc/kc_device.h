@@ -281,7 +281,7 @@ struct PairLookup {
         return reinterpret_cast<const float2*>(base + byte_shl3<B>(w));
     }
 };
-// ... or the lane-sliced copy (see nf4_fill_sliced): offset e * 256 + 8 s for
+// ... or the lane-sliced copy (see sliced_entry_store): offset e * 256 + 8 s for
 // the lane's slot s = lane % 32, formed by one byte permute from the code
 // word and the lane's 8 s (bytes, low to high: 8 s, byte B of w, 0, 0).
 struct SlicedLookup {
@@ -290,20 +290,6 @@ struct SlicedLookup {
     template <int B>
     __device__ __forceinline__ const float2* entry(uint32_t w) const {
         return reinterpret_cast<const float2*>(base + __builtin_amdgcn_perm(w, slot8, 0x0c0c0400u | (B << 8)));
-    }
-};
-
-// ... or a compact copy of 16 interleaved tables (see copy16_entry_store):
-// copy c of entry e at byte e * 128 + 8 c, lane l reading copy l % 16 --
-// one byte-select shift and one OR.  The 32 lanes of an 8-byte LDS pass use
-// 16 bank pairs twice; lanes l and l + 16 collide only when their entries
-// have the same parity.  32 KiB, for kernels that cannot spend 64 KiB.
-struct Copy16Lookup {
-    const char* base;
-    uint32_t copy8;
-    template <int B>
-    __device__ __forceinline__ const float2* entry(uint32_t w) const {
-        return reinterpret_cast<const float2*>(base + (byte_shl<B, 7>(w) | copy8));
     }
 };
 
@@ -464,22 +450,6 @@ __device__ __forceinline__ void sliced_entry_store(float* sliced, float2 e) {
             row[(j + threadIdx.x) & (kNf4Slots - 1)] = e;
         }
     }
-}
-constexpr int kNf4Copies16 = 16;
-constexpr int kNf4Copy16Floats = 2 * kNf4PairEntries * kNf4Copies16;
-// Thread t < 256 writes its entry (pair_entry_fetch) into the 16 copies,
-// copy (j + t) % 16 at step j; the caller publishes with a block barrier.
-__device__ __forceinline__ void copy16_entry_store(float* table, float2 e) {
-    if (threadIdx.x < kNf4PairEntries) {
-        float2* row = reinterpret_cast<float2*>(table) + threadIdx.x * kNf4Copies16;
-#pragma unroll
-        for (int j = 0; j < kNf4Copies16; ++j) {
-            row[(j + threadIdx.x) & (kNf4Copies16 - 1)] = e;
-        }
-    }
-}
-__device__ __forceinline__ Copy16Lookup copy16_lookup(const float* table) {
-    return Copy16Lookup{reinterpret_cast<const char*>(table), (threadIdx.x & (kNf4Copies16 - 1)) * 8u};
 }
 __device__ __forceinline__ SlicedLookup sliced_lookup(const float* sliced) {
     return SlicedLookup{reinterpret_cast<const char*>(sliced), (threadIdx.x & (kNf4Slots - 1)) * 8u};

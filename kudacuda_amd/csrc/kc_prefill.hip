@@ -105,10 +105,11 @@ __device__ __forceinline__ void x_stage(uint8_t* buf, const u32x16& o, int tid) 
 // v_cvt_pk_bf16_f32; the products are finite); element j lands in slot j.
 // lookup4 makes the table reads, scale8_bf16 the products.
 // Both codes of byte b come from one 8-byte read of the LDS pair table, in
-// the block's 16-copy layout (Copy16Lookup: the lane's copy of entry b; its
-// bank conflicts are about a quarter of the single table's -- 64-token
-// prefill 2.90 -> 2.85 ms, bit-identical).
-__device__ __forceinline__ void lookup4(float2* p, uint32_t word, const Copy16Lookup& cb) {
+// the block's lane-sliced layout (SlicedLookup: the lane's slot of entry b,
+// its address one byte permute; no bank conflicts).  Every prefill GEMM runs
+// one block per CU, so its 64 KiB cost no residency: 64-token prefill
+// 2.72 -> 2.65 ms against the 32 KiB 16-copy layout (bit-identical).
+__device__ __forceinline__ void lookup4(float2* p, uint32_t word, const SlicedLookup& cb) {
     p[0] = *cb.template entry<0>(word);
     p[1] = *cb.template entry<1>(word);
     p[2] = *cb.template entry<2>(word);
@@ -131,7 +132,7 @@ __device__ __forceinline__ bf16x8 scale8_bf16(const float2* p, float am) {
 // left the window a chain of ~25 dependent round trips.
 template <int NT>
 __device__ __forceinline__ void gemm_window(const uint8_t* buf, const u32x8& o, floatx4* acc, int r, int q,
-                                            const Copy16Lookup& cb) {
+                                            const SlicedLookup& cb) {
     const float am = __uint_as_float(o[4]);
     float2 p[4][4];
 #pragma unroll
@@ -163,9 +164,9 @@ __global__ __launch_bounds__(64 * W) void nf4_gemm_kernel(Nf4GemmArgs a) {
     static_assert(!kSw || W % 2 == 0, "gate and up waves in pairs");
     constexpr int kFrags = kSw ? W / 2 : W;                  // row fragments of the block per weight
     constexpr int kBlockRows = kFrags * kRowsPerWave;        // output rows of the block
-    __shared__ __attribute__((aligned(16))) float s_cb[kNf4Copy16Floats];
+    __shared__ __attribute__((aligned(16))) float s_cb[kNf4SlicedFloats];
     __shared__ __attribute__((aligned(16))) uint8_t s_x[2][16 * NT * kXPitch];
-    const Copy16Lookup cb = copy16_lookup(s_cb);
+    const SlicedLookup cb = sliced_lookup(s_cb);
     static_assert(64 * W >= kNf4PairEntries, "one pair-table entry per thread");
     const float2 pair_entry = pair_entry_fetch();  // first request: its wait below waits for nothing else
     const int tid = threadIdx.x;
@@ -227,7 +228,7 @@ __global__ __launch_bounds__(64 * W) void nf4_gemm_kernel(Nf4GemmArgs a) {
     u32x16 x2;
     u32x8 w2;
     x_stage<NT>(sx, x0, tx);
-    copy16_entry_store(s_cb, pair_entry);
+    sliced_entry_store(s_cb, pair_entry);
     __syncthreads();
     int buf = 0;
     int64_t kw = k_begin;

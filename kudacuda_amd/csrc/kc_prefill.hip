@@ -126,19 +126,24 @@ __device__ __forceinline__ bf16x8 scale8_bf16(const float2* p, float am) {
     return v;
 }
 
-// One window: every LDS read of the window (16 table reads, 4 NT operand
-// tiles) is issued before the first is used, so the wave waits about one
-// LDS round trip per window; reads issued and consumed a few at a time
-// left the window a chain of ~25 dependent round trips.
-template <int NT>
-__device__ __forceinline__ void gemm_window(const uint8_t* buf, const u32x8& o, floatx4* acc, int r, int q,
-                                            const SlicedLookup& cb) {
-    const float am = __uint_as_float(o[4]);
-    float2 p[4][4];
+// The 16 table reads of one window's codes.
+__device__ __forceinline__ void window_lookups(float2 (&p)[4][4], const u32x8& o, const SlicedLookup& cb) {
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
         lookup4(p[s], o[s], cb);
     }
+}
+
+// One window from its table values `p` (read during the previous window):
+// the window's 4 NT operand tiles are requested together, its weights are
+// formed from `p` while they are in flight, then `p` receives the next
+// window's table reads (codes `on`), which the MFMAs overlap.  Reads issued
+// and consumed a few at a time left the window a chain of ~25 dependent LDS
+// round trips.
+template <int NT>
+__device__ __forceinline__ void gemm_window(const uint8_t* buf, const u32x8& o, float2 (&p)[4][4], const u32x8& on,
+                                            floatx4* acc, int r, int q, const SlicedLookup& cb) {
+    const float am = __uint_as_float(o[4]);
     uint4 B[4][NT];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
@@ -147,13 +152,19 @@ __device__ __forceinline__ void gemm_window(const uint8_t* buf, const u32x8& o, 
             B[s][t] = *reinterpret_cast<const uint4*>(buf + (16 * t + r) * kXPitch + 64 * q + 16 * s);
         }
     }
+    bf16x8 A[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        A[s] = scale8_bf16(p[s], am);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    window_lookups(p, on, cb);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-        const bf16x8 A = scale8_bf16(p[s], am);
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, as_bf16x8(B[s][t]), acc[t], 0, 0, 0);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[s], as_bf16x8(B[s][t]), acc[t], 0, 0, 0);
         }
     }
 }
@@ -230,15 +241,17 @@ __global__ __launch_bounds__(64 * W) void nf4_gemm_kernel(Nf4GemmArgs a) {
     x_stage<NT>(sx, x0, tx);
     sliced_entry_store(s_cb, pair_entry);
     __syncthreads();
+    float2 p[4][4];  // table values of the window about to be computed
+    window_lookups(p, w0, cb);
     int buf = 0;
     int64_t kw = k_begin;
-#define KC_GEMM_STEP(XF, WF, WC, XS)                                               \
+#define KC_GEMM_STEP(XF, WF, WC, WN, XS)                                           \
     {                                                                              \
         const int64_t kf = kw + 2 * kWindow < k_end ? kw + 2 * kWindow : kw;       \
         XF = x_fetch<NT>(xrow, xcol, kf);                                          \
         WF = w_fetch(wrow, arow, kf, q);                                           \
         __builtin_amdgcn_sched_barrier(0); /* requests ahead of the compute */     \
-        gemm_window<NT>(sx + buf * kBuf, WC, acc, r, q, cb);                      \
+        gemm_window<NT>(sx + buf * kBuf, WC, p, WN, acc, r, q, cb);                \
         x_stage<NT>(sx + (buf ^ 1) * kBuf, XS, tx);                                \
         __syncthreads();                                                           \
         buf ^= 1;                                                                  \
@@ -248,9 +261,9 @@ __global__ __launch_bounds__(64 * W) void nf4_gemm_kernel(Nf4GemmArgs a) {
         }                                                                          \
     }
     while (true) {
-        KC_GEMM_STEP(x2, w2, w0, x1)
-        KC_GEMM_STEP(x0, w0, w1, x2)
-        KC_GEMM_STEP(x1, w1, w2, x0)
+        KC_GEMM_STEP(x2, w2, w0, w1, x1)
+        KC_GEMM_STEP(x0, w0, w1, w2, x2)
+        KC_GEMM_STEP(x1, w1, w2, w0, x0)
     }
 #undef KC_GEMM_STEP
 

@@ -425,14 +425,19 @@ __global__ __launch_bounds__(256) void qkv_rope_reduce_kernel(Nf4GemmArgs a, int
     const int64_t plane = a.m * a.n;
     if (u >= q_units + k_units) {
         const int64_t c = a.q_rows + a.kv_rows + 4 * (u - q_units - k_units);  // v column
+        const int64_t cv = c - a.q_rows - a.kv_rows;
+        // the bias is read unconditionally (a stand-in address when there is
+        // none) so that its request goes out with the partials'
+        const uint16_t* b = a.seg_bias[2];
+        const uint2 braw = *reinterpret_cast<const uint2*>(b != nullptr ? b + cv : a.x);
         float vs[4];
         split_sum<4>(src + c, plane, S, vs);
-        const int64_t cv = c - a.q_rows - a.kv_rows;
-        const uint16_t* b = a.seg_bias[2];
+        const uint16_t bb[4] = {static_cast<uint16_t>(braw.x), static_cast<uint16_t>(braw.x >> 16),
+                                static_cast<uint16_t>(braw.y), static_cast<uint16_t>(braw.y >> 16)};
         uint16_t h[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            h[i] = Bf16::store(b != nullptr ? vs[i] + Bf16::load(b[cv + i]) : vs[i]);
+            h[i] = Bf16::store(b != nullptr ? vs[i] + Bf16::load(bb[i]) : vs[i]);
         }
         uint16_t* dst = a.vcache + ((cv / 128) * a.capacity + pos) * 128 + cv % 128;
         *reinterpret_cast<uint2*>(dst) = make_uint2(static_cast<uint32_t>(h[0]) | (static_cast<uint32_t>(h[1]) << 16),
@@ -444,21 +449,28 @@ __global__ __launch_bounds__(256) void qkv_rope_reduce_kernel(Nf4GemmArgs a, int
     const int64_t head = uu / 32;
     const int d = static_cast<int>(uu % 32) * 2;
     const int64_t c0 = (is_q ? 0 : a.q_rows) + head * 128 + d;  // partial column of (d, d + 1)
+    const uint16_t* b = is_q ? a.seg_bias[0] : a.seg_bias[1];
+    const int64_t cb0 = head * 128 + d;  // column within the segment
+    // bias (a stand-in address when there is none) and rotary factors are
+    // requested with the partials, not after them
+    const uint32_t blo = *reinterpret_cast<const uint32_t*>(b != nullptr ? b + cb0 : a.x);
+    const uint32_t bhi = *reinterpret_cast<const uint32_t*>(b != nullptr ? b + cb0 + 64 : a.x);
+    const float2 cs = *reinterpret_cast<const float2*>(a.rope_cos + pos * 64 + d);
+    const float2 sn = *reinterpret_cast<const float2*>(a.rope_sin + pos * 64 + d);
     float lov[2], hiv[2];
     split_sum<2>(src + c0, plane, S, lov);
     split_sum<2>(src + c0 + 64, plane, S, hiv);
     const float2 lo = make_float2(lov[0], lov[1]);
     const float2 hi = make_float2(hiv[0], hiv[1]);
-    const uint16_t* b = is_q ? a.seg_bias[0] : a.seg_bias[1];
-    const int64_t cb0 = head * 128 + d;  // column within the segment
-    const float l0 = Bf16::load(Bf16::store(b != nullptr ? lo.x + Bf16::load(b[cb0]) : lo.x));
-    const float l1 = Bf16::load(Bf16::store(b != nullptr ? lo.y + Bf16::load(b[cb0 + 1]) : lo.y));
-    const float h0 = Bf16::load(Bf16::store(b != nullptr ? hi.x + Bf16::load(b[cb0 + 64]) : hi.x));
-    const float h1 = Bf16::load(Bf16::store(b != nullptr ? hi.y + Bf16::load(b[cb0 + 65]) : hi.y));
-    const float c_0 = a.rope_cos[pos * 64 + d];
-    const float c_1 = a.rope_cos[pos * 64 + d + 1];
-    const float s_0 = a.rope_sin[pos * 64 + d];
-    const float s_1 = a.rope_sin[pos * 64 + d + 1];
+    const bool hb = b != nullptr;
+    const float l0 = Bf16::load(Bf16::store(hb ? lo.x + Bf16::load(static_cast<uint16_t>(blo)) : lo.x));
+    const float l1 = Bf16::load(Bf16::store(hb ? lo.y + Bf16::load(static_cast<uint16_t>(blo >> 16)) : lo.y));
+    const float h0 = Bf16::load(Bf16::store(hb ? hi.x + Bf16::load(static_cast<uint16_t>(bhi)) : hi.x));
+    const float h1 = Bf16::load(Bf16::store(hb ? hi.y + Bf16::load(static_cast<uint16_t>(bhi >> 16)) : hi.y));
+    const float c_0 = cs.x;
+    const float c_1 = cs.y;
+    const float s_0 = sn.x;
+    const float s_1 = sn.y;
     const uint32_t rl = static_cast<uint32_t>(Bf16::store((l0 * c_0) - (h0 * s_0))) |
                         (static_cast<uint32_t>(Bf16::store((l1 * c_1) - (h1 * s_1))) << 16);
     const uint32_t rh = static_cast<uint32_t>(Bf16::store((h0 * c_0) + (l0 * s_0))) |
@@ -481,9 +493,12 @@ __global__ __launch_bounds__(256) void residual_norm_reduce_kernel(Nf4GemmArgs a
     const int64_t c = 8 * t;
     const float* src = a.partials + m * a.n + c;
     const int64_t plane = a.m * a.n;
+    // residual and gamma (the residual again when there is no norm) are
+    // requested with the partials, so no load waits behind the barrier below
+    const uint4 rv = *reinterpret_cast<const uint4*>(a.residual + m * a.n + c);
+    const uint4 gv = *reinterpret_cast<const uint4*>(a.norm_gamma != nullptr ? a.norm_gamma + c : a.residual + m * a.n + c);
     float v[8];
     split_sum<8>(src, plane, S, v);
-    const uint4 rv = *reinterpret_cast<const uint4*>(a.residual + m * a.n + c);
     float res[8];
     unpack8<Bf16>(rv, res);
     float h[8];
@@ -512,7 +527,7 @@ __global__ __launch_bounds__(256) void residual_norm_reduce_kernel(Nf4GemmArgs a
     __syncthreads();
     const float r = inv_rms((s_ss[0] + s_ss[1]) + (s_ss[2] + s_ss[3]), 2048.0f, a.eps);
     float g[8];
-    unpack8<Bf16>(*reinterpret_cast<const uint4*>(a.norm_gamma + c), g);
+    unpack8<Bf16>(gv, g);
 #pragma unroll
     for (int i = 0; i < 8; i += 2) {
         const uint32_t lo = Bf16::store((h[i] * r) * g[i]);

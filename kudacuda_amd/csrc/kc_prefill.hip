@@ -720,22 +720,29 @@ __global__ __launch_bounds__(256) void prefill_norm_kernel(PrefillNormArgs a) {
 // grid m: thread t rotates the q pairs t, t+256, t+512, t+768 (head p/64,
 // dim p%64), k pair t (< 128) and copies k/v element t (< 256) to the caches.
 constexpr int kAttnGroups = 32;  // 16-lane groups of a 512-thread block
-constexpr int kAttnHeads = 8;
+constexpr int kAttnHeads = 8;    // query heads per KV head
+constexpr int kAttnBlockHeads = 4;
 constexpr int kAttnDim = 128;
 
-// grid (m, 2 KV heads), 512 threads.  Query row r (position start + r) of the
-// 8 heads of KV head g over cache rows [0, start + r], in rounds of 32 tokens
+// grid (m, 2 KV heads, 2 head halves), 512 threads.  Query row r (position
+// start + r) of query heads 4z .. 4z + 3 of KV head g (8 per KV head; each
+// head's arithmetic is independent of the others', so halving the heads per
+// block doubles the blocks -- 256 for 64 tokens -- and leaves every result as
+// it was) over cache rows [0, start + r], in rounds of 32 tokens
 // (one per 16-lane group): scores by 8-dim partial dots and the 16-lane DPP
 // butterfly (log2 domain), then per head m_new = max(m, round max), weights
 // exp2(s - m_new), rescale exp2(m - m_new) of the running sum and accumulator,
 // weighted V rows from LDS in token order.  out = bf16(acc / sum).
 __global__ __launch_bounds__(512) void prefill_attention_kernel(PrefillAttnArgs a) {
-    __shared__ __attribute__((aligned(16))) float s_sc[2][kAttnHeads][kAttnGroups];
-    __shared__ __attribute__((aligned(16))) float s_w[2][kAttnHeads][kAttnGroups];
-    __shared__ float s_corr[2][kAttnHeads];
+    constexpr int H = kAttnBlockHeads;
+    static_assert(H * kAttnDim == 512, "one thread per (head, dim) in the weighted sum");
+    __shared__ __attribute__((aligned(16))) float s_sc[2][H][kAttnGroups];
+    __shared__ __attribute__((aligned(16))) float s_w[2][H][kAttnGroups];
+    __shared__ float s_corr[2][H];
     __shared__ __attribute__((aligned(16))) float s_v[2][kAttnGroups][kAttnDim];
     const int64_t row = blockIdx.x;
     const int g = blockIdx.y;
+    const int h0 = g * kAttnHeads + static_cast<int>(blockIdx.z) * H;  // first query head of the block
     const int lane = threadIdx.x & 63;
     const int gi = threadIdx.x >> 4;
     const int li = lane & 15;
@@ -744,17 +751,17 @@ __global__ __launch_bounds__(512) void prefill_attention_kernel(PrefillAttnArgs 
     const uint16_t* kbase = a.kcache + static_cast<int64_t>(g) * a.capacity * kAttnDim + 8 * li;
     const uint16_t* vbase = a.vcache + static_cast<int64_t>(g) * a.capacity * kAttnDim + 8 * li;
 
-    float q[kAttnHeads][8];
+    float q[H][8];
 #pragma unroll
-    for (int hl = 0; hl < kAttnHeads; ++hl) {
-        const uint4 qr = *reinterpret_cast<const uint4*>(a.q + row * 2048 + (g * kAttnHeads + hl) * kAttnDim + 8 * li);
+    for (int hl = 0; hl < H; ++hl) {
+        const uint4 qr = *reinterpret_cast<const uint4*>(a.q + row * 2048 + (h0 + hl) * kAttnDim + 8 * li);
         unpack8<Bf16>(qr, q[hl]);
     }
-    const int sm_h = threadIdx.x / kAttnGroups;  // softmax threads (t < 256)
+    const int sm_h = threadIdx.x / kAttnGroups;  // softmax threads (t < 128)
     const int sm_x = threadIdx.x % kAttnGroups;
     float m_run = -__builtin_huge_valf();
-    float acc[2] = {0.0f, 0.0f};
-    float l_run[2] = {0.0f, 0.0f};
+    float acc = 0.0f;
+    float l_run = 0.0f;
     const int nround = static_cast<int>((L + kAttnGroups - 1) / kAttnGroups);
     int64_t t = gi < last ? gi : last;
     uint4 kA = *reinterpret_cast<const uint4*>(kbase + t * kAttnDim);
@@ -769,9 +776,9 @@ __global__ __launch_bounds__(512) void prefill_attention_kernel(PrefillAttnArgs 
         float kf[8], vf[8];
         unpack8<Bf16>(kA, kf);
         unpack8<Bf16>(vA, vf);
-        float dots[kAttnHeads];
+        float dots[H];
 #pragma unroll
-        for (int hl = 0; hl < kAttnHeads; ++hl) {
+        for (int hl = 0; hl < H; ++hl) {
             float acc_d = 0.0f;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
@@ -781,17 +788,17 @@ __global__ __launch_bounds__(512) void prefill_attention_kernel(PrefillAttnArgs 
         }
         float mine = dots[0];
 #pragma unroll
-        for (int hl = 1; hl < kAttnHeads; ++hl) {
+        for (int hl = 1; hl < H; ++hl) {
             mine = li == hl ? dots[hl] : mine;
         }
-        if (li < kAttnHeads) {
+        if (li < H) {
             s_sc[buf][li][gi] = mine * a.qk_scale_log2;
         }
         float4* vrow = reinterpret_cast<float4*>(&s_v[buf][gi][8 * li]);
         vrow[0] = make_float4(vf[0], vf[1], vf[2], vf[3]);
         vrow[1] = make_float4(vf[4], vf[5], vf[6], vf[7]);
         __syncthreads();
-        if (threadIdx.x < kAttnGroups * kAttnHeads) {
+        if (threadIdx.x < kAttnGroups * H) {
             float mr = -__builtin_huge_valf();
             for (int x = 0; x < nvalid; ++x) {
                 mr = fmaxf(mr, s_sc[buf][sm_h][x]);
@@ -804,29 +811,27 @@ __global__ __launch_bounds__(512) void prefill_attention_kernel(PrefillAttnArgs 
             m_run = m_new;
         }
         __syncthreads();
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            const int hl = half * 4 + threadIdx.x / kAttnDim;
+        {
+            const int hl = threadIdx.x / kAttnDim;
             const int d = threadIdx.x % kAttnDim;
             const float corr = s_corr[buf][hl];
-            float av = acc[half] * corr;
-            float lv = l_run[half] * corr;
+            float av = acc * corr;
+            float lv = l_run * corr;
             for (int x = 0; x < nvalid; ++x) {
                 const float w = s_w[buf][hl][x];
                 av = fmaf(w, s_v[buf][x][d], av);
                 lv = lv + w;
             }
-            acc[half] = av;
-            l_run[half] = lv;
+            acc = av;
+            l_run = lv;
         }
         kA = kB;
         vA = vB;
     }
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-        const int hl = half * 4 + threadIdx.x / kAttnDim;
+    {
+        const int hl = threadIdx.x / kAttnDim;
         const int d = threadIdx.x % kAttnDim;
-        a.out[row * 2048 + (g * kAttnHeads + hl) * kAttnDim + d] = Bf16::store(acc[half] / l_run[half]);
+        a.out[row * 2048 + (h0 + hl) * kAttnDim + d] = Bf16::store(acc / l_run);
     }
 }
 
@@ -862,7 +867,8 @@ hipError_t launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t stream
         a.vcache == nullptr || a.out == nullptr) {
         return hipErrorInvalidValue;
     }
-    hipLaunchKernelGGL(prefill_attention_kernel, dim3(static_cast<unsigned>(a.m), 2), dim3(512), 0, stream, a);
+    hipLaunchKernelGGL(prefill_attention_kernel, dim3(static_cast<unsigned>(a.m), 2, kAttnHeads / kAttnBlockHeads),
+                       dim3(512), 0, stream, a);
     return hipGetLastError();
 }
 

@@ -799,12 +799,16 @@ __global__ __launch_bounds__(512) void prefill_attention_kernel(PrefillAttnArgs 
         vrow[1] = make_float4(vf[4], vf[5], vf[6], vf[7]);
         __syncthreads();
         if (threadIdx.x < kAttnGroups * H) {
-            float mr = -__builtin_huge_valf();
-            for (int x = 0; x < nvalid; ++x) {
-                mr = fmaxf(mr, s_sc[buf][sm_h][x]);
+            // the round's maximum per head: a 32-lane butterfly over the
+            // head's softmax threads (a maximum is exact in any order)
+            const float sc = s_sc[buf][sm_h][sm_x];
+            float mr = sm_x < nvalid ? sc : -__builtin_huge_valf();
+#pragma unroll
+            for (int o = 16; o >= 1; o >>= 1) {
+                mr = fmaxf(mr, __shfl_xor(mr, o, kAttnGroups));
             }
             const float m_new = fmaxf(m_run, mr);
-            s_w[buf][sm_h][sm_x] = sm_x < nvalid ? exp2_fixed(s_sc[buf][sm_h][sm_x] - m_new) : 0.0f;
+            s_w[buf][sm_h][sm_x] = sm_x < nvalid ? exp2_fixed(sc - m_new) : 0.0f;
             if (sm_x == 0) {
                 s_corr[buf][sm_h] = exp2_fixed(m_run - m_new);
             }

@@ -73,6 +73,13 @@ constexpr int kDim = 128;
 constexpr int kPartialStride = kGqaPartialStride;
 static_assert(kPartialStride == 2 + kDim, "partial layout: max, sum, acc[128]");
 constexpr int kInKernelSplits = 32;
+// With kv_len in device memory, only splits below this request their rows
+// before kv_len is known: the decode step's grid covers every split the cache
+// bucket could need (64 at 2048 tokens) while decode lengths need a few, and
+// the rows the idle blocks requested cost the step ~14 us of 1 ms (their
+// traffic lands beside the live blocks' and the next kernel's).  16 splits
+// cover decode lengths up to 512 tokens; later splits wait for kv_len first.
+constexpr int64_t kSpeculativeSplits = 16;
 constexpr int kMergeMaxSplits = 256;  // one split's max and sum per merge thread
 static_assert(kGqaSplitCap <= kMergeMaxSplits, "every plan's split count (split_limit only lowers it)");
 constexpr int kMergeDims = 16;              // dims per merge block
@@ -238,12 +245,15 @@ void gqa_partial_kernel(const uint16_t* k_rows, const uint16_t* v_rows, const ui
     }
     const bool device_len = a.kv_len_device != nullptr;
     const int64_t c_guess = device_len ? kRound : gqa_split_tokens(read_kv_len(a), a.split_cap);
+    // a host kv_len gives the live splits exactly; a device one is guessed
+    // (kSpeculativeSplits)
+    const bool spec = device_len ? s < kSpeculativeSplits : s * c_guess < read_kv_len(a);
     // Rows are always requested two at a time in this order (round r's K, V,
     // then round r+1's), rows past the split re-reading its last row, so the
     // waves' memory counters see the same sequence every round and each round
     // waits only for its own rows.
     uint4 k0, v0, k1, v1;
-    {
+    if (spec) {
         // the guessed split's own rows only (a one-round split re-reads its
         // last row instead of the next split's first round)
         const int64_t g0 = s * c_guess;
@@ -268,7 +278,7 @@ void gqa_partial_kernel(const uint16_t* k_rows, const uint16_t* v_rows, const ui
     }
     const int64_t t0 = s * C;
     const int64_t tend = t0 + C < L ? t0 + C : L;
-    if (C != c_guess) {
+    if (!spec || C != c_guess) {
         load_row(kbase, vbase, t0 + gi, tend, k0, v0);
         load_row(kbase, vbase, t0 + kRound + gi, tend, k1, v1);
     }

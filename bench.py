@@ -33,6 +33,9 @@ same way.
 
 Usage: python bench.py [--gpus 1] [--steps 128] [--warmup 16]
        python bench.py --decode-only   (the run profiles/roofline_rocprof.json is traced from)
+       python bench.py --context-sweep (decode step time by cached tokens, not the metric: the
+                                        KV caches are filled with random rows up to each start
+                                        position, then 32 replays from it are timed)
 """
 
 from __future__ import annotations
@@ -282,6 +285,44 @@ def cpu_baseline(seconds: float, threads: int) -> dict:
     }
 
 
+SWEEP_TOKENS = (64, 160, 200, 240, 300, 600, 1000, 1500, 1950)
+SWEEP_STEPS = 32
+
+
+def context_sweep(model, torch, synthetic, starts: list[int], seed: int, vocab: int) -> int:
+    """Decode step time by cached tokens: the KV caches of every layer are
+    filled with random rows (the step's time does not depend on their values),
+    then for each start the step is set there and SWEEP_STEPS graph replays
+    are timed with HIP events on the model stream."""
+
+    if any(s < 1 or s + SWEEP_STEPS + 2 >= KV_BUCKET for s in starts):
+        print(f"context sweep starts must lie in 1..{KV_BUCKET - SWEEP_STEPS - 3}", file=sys.stderr)
+        return 2
+    gen = torch.Generator(device=model.tokens.device).manual_seed(seed)
+    with torch.cuda.stream(model.stream):
+        for layer in model.layers:
+            for name in ("key_cache", "value_cache"):
+                cache = layer[name]
+                cache.copy_((torch.randn(cache.shape, generator=gen, device=cache.device) * 0.5).to(cache.dtype))
+    model.stream.synchronize()
+    model.capture()
+    ms = {}
+    for start in starts:
+        model.reset(synthetic.prompt_ids(seed, start + 1, vocab), start_step=start)
+        model.replay(2)
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(model.stream)
+        model.replay(SWEEP_STEPS)
+        b.record(model.stream)
+        b.synchronize()
+        ms[str(start)] = round(a.elapsed_time(b) / SWEEP_STEPS, 4)
+    print(json.dumps({"context_sweep_ms_per_step": ms, "steps_per_start": SWEEP_STEPS, "kv_bucket": KV_BUCKET,
+                      "what": "decode step time with the given number of tokens cached (random cache rows); "
+                              "not the benchmark metric"}), flush=True)
+    return 0
+
+
 def main(argv: list[str] | None = None) -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -296,6 +337,9 @@ def main(argv: list[str] | None = None) -> int:
     parser.add_argument("--decode-only", action="store_true",
                         help="profiling run: the prompt, warm-up and timed decode steps and the per-kernel loop only "
                              "(no per-token loop, prefill, per-config cases or CPU baselines)")
+    parser.add_argument("--context-sweep", type=int, nargs="*", metavar="TOKENS",
+                        help="decode step time with this many tokens cached (default list when none given); "
+                             "prints one JSON line and skips the benchmark")
     args = parser.parse_args(argv)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -321,6 +365,8 @@ def main(argv: list[str] | None = None) -> int:
                                       token_capacity=KV_BUCKET, threads=threads)
     print(f"[bench] model built in {time.time() - t0:.1f}s ({args.layers} layers)", file=sys.stderr, flush=True)
     stream = model.stream
+    if args.context_sweep is not None:
+        return context_sweep(model, torch, synthetic, args.context_sweep or list(SWEEP_TOKENS), args.seed, cfg.vocab)
     prompt = synthetic.prompt_ids(args.seed, PROMPT_LEN, cfg.vocab)
 
     # prompt: steps 0..62 (lm_head skipped on device until the last prompt token)

@@ -27,7 +27,11 @@ enum class RowMode { kGemv = 0, kQkv = 1, kQkvRope = 2, kSwiGlu = 3 };
 constexpr int kGqaPartialStride = 130;
 constexpr int kGqaRoundTokens = 32;      // tokens of one round (one per 16-lane group of a block)
 constexpr int64_t kGqaSplitCap = 256;    // most splits per KV head of an uncapped plan
-constexpr int kGqaMaxDefer = 8;          // most splits a consumer merges
+// Most splits a consumer merges.  Each slot costs o_proj ~0.1 us per layer
+// at every length (its requests re-read split 0 when fewer are live); 6
+// covers one-round splits up to 192 tokens, after which the attention
+// kernel's ticket merge takes over.
+constexpr int kGqaMaxDefer = 6;
 constexpr int kGqaMergeGroup = 16;       // merges sum splits in groups of this many, then the groups
 // Split cap of the decode step's plan: every split count it can reach is
 // merged by o_proj (deferred) or by the in-kernel ticket, so the step's graph

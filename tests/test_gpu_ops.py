@@ -446,7 +446,7 @@ def test_handle_scratch_is_refused_to_a_second_busy_stream(torch_gpu, native, st
 
     stream.synchronize()
     with torch.cuda.stream(stream):
-        torch.cuda._sleep(100_000_000)  # keeps the first stream busy (bounded spin, ~0.05 s)
+        torch.cuda._sleep(1_000_000_000)  # keeps the first stream busy (bounded spin, ~0.4-0.5 s)
     assert lm_head(0, stream) == 0
     assert lm_head(1, other) == 1 and "scratch" in native.error()
     stream.synchronize()

@@ -205,9 +205,10 @@ __device__ __forceinline__ float2 wave_sum2(float a, float b) {
 //      (global_load_* ... sc1).
 // Steps 1, 2 and 4 alone carry the data on this hardware; step 3's fences
 // make the hand-over correct by the memory model instead of by those cache
-// bits, for ~0.2 us per launch of a few publishing blocks (each release's L2
+// bits, for ~0.2 us per launch of a few publishing blocks.  Each release's L2
 // write-back costs ~0.3 us and those of one XCD serialise, so a launch with
-// hundreds of publishing blocks keeps a relaxed ticket: lm_head).
+// hundreds of publishing blocks (lm_head) takes no ticket: its blocks write
+// with plain stores and a second kernel reads them after the kernel boundary.
 __device__ __forceinline__ void store_agent(float* p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

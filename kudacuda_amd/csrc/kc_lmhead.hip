@@ -8,7 +8,11 @@
 // argmax runs on the rounded values with the lowest index winning ties, as
 // torch.argmax does on the reference's logits
 // (tools/benchmark/benchmark_gemma.py:350).  Block winners go to a small
-// workspace and the last block (device-scope ticket) picks the token.
+// workspace with plain stores; a one-block second kernel on the same stream
+// reads them (the kernel boundary orders the stores before its loads) and
+// picks the token.  (A "last block" ticket inside the GEMV kernel cost as much
+// as that second launch and needed device-scope fences on every block to be
+// correct by the memory model.)
 //
 // When `control` is given the launch also does the per-token decode
 // bookkeeping on device: during the prompt (step + 1 < prompt_len) the GEMV is
@@ -63,7 +67,6 @@ __global__ __launch_bounds__(kLmThreads) void lm_head_kernel(const uint16_t* wei
     a.vocab = vocab;
     __shared__ float s_val[kLmThreads / 64];
     __shared__ int32_t s_idx[kLmThreads / 64];
-    __shared__ int s_last;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
 
@@ -193,35 +196,36 @@ __global__ __launch_bounds__(kLmThreads) void lm_head_kernel(const uint16_t* wei
                     best_idx = s_idx[i];
                 }
             }
-            store_agent(a.block_best + 2 * blockIdx.x, best);
-            store_agent(a.block_best + 2 * blockIdx.x + 1, __int_as_float(best_idx));
+            a.block_best[2 * blockIdx.x] = best;
+            a.block_best[2 * blockIdx.x + 1] = __int_as_float(best_idx);
         }
     }
+}
 
-    // block winners travel through agent-scope atomic stores (written through
-    // the L2) that every wave waits for, and agent-scope loads (which miss
-    // the non-coherent caches); the ticket is a relaxed fetch-add.  768
-    // publishing blocks make take_ticket's release too dear here: its L2
-    // write-back (buffer_wbl2 sc1) costs ~0.3 us and the blocks of an XCD
-    // serialise on it, 107 -> 135 us per token.
-    wait_own_stores();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t prev = atomicAdd(a.counter, 1u);
-        s_last = prev == gridDim.x - 1 ? 1 : 0;
+// The token from the GEMV launch's `nblocks` block winners, and the decode
+// bookkeeping.  One block; the winners' order does not matter (better() is
+// the first-max rule on (value, index) pairs).
+__global__ __launch_bounds__(kLmThreads) void lm_head_finish_kernel(LmHeadArgs a, int nblocks) {
+    __shared__ float s_val[kLmThreads / 64];
+    __shared__ int32_t s_idx[kLmThreads / 64];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    int32_t step = 0;
+    bool active = true;
+    bool stopped = false;
+    if (a.control != nullptr) {
+        step = a.control[0];
+        stopped = a.control[4] != 0;
+        active = !stopped && step + 1 >= a.control[1];
     }
-    __syncthreads();
-    if (s_last == 0) {
-        return;
-    }
+    float best = -__builtin_huge_valf();
+    int32_t best_idx = 0x7fffffff;
     if (active) {
-        best = -__builtin_huge_valf();
-        best_idx = 0x7fffffff;
-        for (int b = threadIdx.x; b < static_cast<int>(gridDim.x); b += kLmThreads) {
-            const float v = load_agent(a.block_best + 2 * b);
-            const int32_t i = __float_as_int(load_agent(a.block_best + 2 * b + 1));
-            if (better(v, i, best, best_idx)) {
-                best = v;
+        for (int b = threadIdx.x; b < nblocks; b += kLmThreads) {
+            const float2 e = reinterpret_cast<const float2*>(a.block_best)[b];
+            const int32_t i = __float_as_int(e.y);
+            if (better(e.x, i, best, best_idx)) {
+                best = e.x;
                 best_idx = i;
             }
         }
@@ -266,7 +270,6 @@ __global__ __launch_bounds__(kLmThreads) void lm_head_kernel(const uint16_t* wei
             }
             a.control[0] = next;
         }
-        store_agent(a.counter, 0u);
     }
 }
 
@@ -282,6 +285,11 @@ hipError_t launch_lm_head_argmax(const LmHeadArgs& a, hipStream_t stream) {
     }
     hipLaunchKernelGGL(lm_head_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kLmThreads), 0, stream, a.weight, a.x,
                        a.gamma, a.vocab, a);
+    const hipError_t st = hipGetLastError();
+    if (st != hipSuccess) {
+        return st;
+    }
+    hipLaunchKernelGGL(lm_head_finish_kernel, dim3(1), dim3(kLmThreads), 0, stream, a, static_cast<int>(blocks));
     return hipGetLastError();
 }
 

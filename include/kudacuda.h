@@ -16,7 +16,11 @@
  *     attention/argmax/GEMM scratch are not shared safely between concurrent
  *     calls; a call that uses that scratch on another stream than the last
  *     such call returns 1 until that call's launch has completed (an event
- *     the handle records behind it; captures are not checked).
+ *     the handle records behind it).  Calls recorded into a capture are
+ *     checked when the graph runs: kudacuda_replay_graph claims the scratch
+ *     for a graph captured by kudacuda_begin_capture that holds such calls;
+ *     a graph captured by other means shares the scratch unchecked, so its
+ *     replays must not overlap other users of the same handle.
  * Activations named "_bf16" are bfloat16; the reference's un-suffixed NF4 QKV
  * and GQA entry points keep their fp16 activations.
  */
@@ -272,7 +276,9 @@ KUDACUDA_API int64_t kudacuda_lm_head_workspace_floats(void);
 
 /* ------------------------------------------------------------- graphs */
 /* reference include/kudacuda.h:257-263 — capture the caller's stream (global
- * mode), instantiate on end, replay with hipGraphLaunch, reset. */
+ * mode), instantiate on end, replay with hipGraphLaunch, reset.  A replay of
+ * a graph holding scratch-using calls is refused (1) like an eager call while
+ * the handle's last scratch user on another stream has work queued. */
 KUDACUDA_API int kudacuda_begin_capture(void* handle, uint64_t stream);
 KUDACUDA_API int kudacuda_end_capture(void* handle, uint64_t stream);
 KUDACUDA_API int kudacuda_replay_graph(void* handle, uint64_t stream);

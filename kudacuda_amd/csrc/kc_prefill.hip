@@ -135,11 +135,16 @@ __device__ __forceinline__ void window_lookups(float2 (&p)[4][4], const u32x8& o
 }
 
 // One window from its table values `p` (read during the previous window):
-// the window's 4 NT operand tiles are requested together, its weights are
-// formed from `p` while they are in flight, then `p` receives the next
-// window's table reads (codes `on`), which the MFMAs overlap.  Reads issued
-// and consumed a few at a time left the window a chain of ~25 dependent LDS
-// round trips.
+// the window's 4 NT operand tiles are requested together and the first
+// k-step's weights formed while they are in flight; each MFMA is then
+// followed by one weight pair of the next k-step, so the products and
+// conversions issue while the matrix core works; after the last MFMA `p`
+// receives the next window's table reads (codes `on`), whose latency the
+// block barrier that ends the window covers.  Reads issued and consumed a
+// few at a time left the window a chain of ~25 dependent LDS round trips.
+// Against all weights formed before the first MFMA with the next table reads
+// ahead of the MFMAs: 64-token prefill 2.53 -> 2.48 ms on one box, ~0.5 % on
+// two others (bit-identical).
 template <int NT>
 __device__ __forceinline__ void gemm_window(const uint8_t* buf, const u32x8& o, float2 (&p)[4][4], const u32x8& on,
                                             floatx4* acc, int r, int q, const SlicedLookup& cb) {
@@ -153,20 +158,24 @@ __device__ __forceinline__ void gemm_window(const uint8_t* buf, const u32x8& o, 
         }
     }
     bf16x8 A[4];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-        A[s] = scale8_bf16(p[s], am);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    window_lookups(p, on, cb);
+    A[0] = scale8_bf16(p[0], am);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[s], as_bf16x8(B[s][t]), acc[t], 0, 0, 0);
+        for (int t = 0; t < 4; ++t) {
+            if (t < NT) {
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[s], as_bf16x8(B[s][t]), acc[t], 0, 0, 0);
+            }
+            if (s < 3) {
+                A[s + 1][2 * t] = static_cast<__bf16>(p[s + 1][t].x * am);
+                A[s + 1][2 * t + 1] = static_cast<__bf16>(p[s + 1][t].y * am);
+            }
+            __builtin_amdgcn_sched_barrier(0);  // keeps each MFMA and its pair together
         }
     }
+    window_lookups(p, on, cb);
+    __builtin_amdgcn_sched_barrier(0);  // the reads stay ahead of the x staging that follows
 }
 
 template <GemmEpi EPI, int NT, int W = kGemmWaves>

@@ -128,6 +128,11 @@ struct Handle {
     hipStream_t scratch_stream = nullptr;
     hipEvent_t scratch_event = nullptr;
     bool scratch_used = false;
+    // a scratch-using call was recorded into the capture begun by
+    // kudacuda_begin_capture / the instantiated graph holds one: its replays
+    // take part in the claim like eager calls
+    bool capture_uses_scratch = false;
+    bool graph_uses_scratch = false;
 };
 
 Handle* as_handle(void* raw) { return reinterpret_cast<Handle*>(raw); }
@@ -158,7 +163,11 @@ bool ready(Handle* h, const char* symbol) {
 // previous launch may still be using the scratch).  Only the handle's event
 // is queried: the previous stream may have been destroyed since.  A call on
 // the same stream is ordered after the previous one.  Launches recorded into
-// a stream capture are not checked: they run when the graph is replayed.
+// a stream capture are not checked: they run when the graph is replayed.  A
+// graph captured through kudacuda_begin_capture that holds such launches is
+// checked at kudacuda_replay_graph instead (claimed on the replay stream, the
+// event recorded behind the replay); graphs captured by other means share
+// the handle's scratch unchecked, so their replays must not overlap.
 bool capturing(hipStream_t s) {
     if (s == nullptr) {
         return false;  // the legacy stream is never captured (and asking it during a global capture is unsafe)
@@ -170,7 +179,11 @@ bool capturing(hipStream_t s) {
 }
 
 bool claim_scratch(Handle* h, const char* symbol, hipStream_t s) {
-    if (capturing(s) || !h->scratch_used || s == h->scratch_stream) {
+    if (capturing(s)) {
+        h->capture_uses_scratch = true;
+        return true;
+    }
+    if (!h->scratch_used || s == h->scratch_stream) {
         return true;
     }
     const hipError_t q = hipEventQuery(h->scratch_event);
@@ -1378,6 +1391,7 @@ int kudacuda_begin_capture(void* raw, uint64_t stream) {
         return 1;
     }
     h->capturing = true;
+    h->capture_uses_scratch = false;
     h->last_error.clear();
     return 0;
 }
@@ -1408,6 +1422,7 @@ int kudacuda_end_capture(void* raw, uint64_t stream) {
         h->set_hip_error("hipGraphInstantiate", inst);
         return 1;
     }
+    h->graph_uses_scratch = h->capture_uses_scratch;
     h->last_error.clear();
     return 0;
 }
@@ -1420,7 +1435,14 @@ int kudacuda_replay_graph(void* raw, uint64_t stream) {
         }
         return 1;
     }
-    return finish(h, "hipGraphLaunch", hipGraphLaunch(h->graph_exec, as_stream(stream)));
+    if (!h->graph_uses_scratch) {
+        return finish(h, "hipGraphLaunch", hipGraphLaunch(h->graph_exec, as_stream(stream)));
+    }
+    if (!claim_scratch(h, "kudacuda_replay_graph", as_stream(stream))) {
+        return 1;
+    }
+    return finish(h, "hipGraphLaunch",
+                  scratch_launched(h, as_stream(stream), hipGraphLaunch(h->graph_exec, as_stream(stream))));
 }
 
 int kudacuda_reset_graph(void* raw) {
@@ -1448,6 +1470,7 @@ int kudacuda_reset_graph(void* raw) {
         }
         h->graph = nullptr;
     }
+    h->graph_uses_scratch = false;
     h->last_error.clear();
     return 0;
 }

@@ -458,6 +458,53 @@ def test_handle_scratch_is_refused_to_a_second_busy_stream(torch_gpu, native, st
     stream.synchronize()
 
 
+def test_handle_graph_replay_takes_part_in_the_scratch_claim(torch_gpu, native, stream):
+    """A graph captured through kudacuda_begin_capture that holds a
+    scratch-using call is claimed at each kudacuda_replay_graph like an eager
+    call: refused while another stream's scratch work is queued, and its own
+    replay keeps an eager call on another stream out until it completes."""
+    torch = torch_gpu
+    if not hasattr(torch.cuda, "_sleep"):
+        pytest.skip("this torch has no device sleep to keep a stream busy")
+    vocab = 4096
+    x = synthetic.f32_to_bf16_bits(synthetic.normal(SEED, (13,), (2048,), 1.0))
+    emb = synthetic.embedding_bits(SEED, vocab=vocab)
+    d_x, d_e = dev(torch, x), dev(torch, emb)
+    outs = [(empty(torch, vocab, "u16"), empty(torch, 1, "i32")) for _ in range(2)]
+    other = torch.cuda.Stream()
+    lib, h = native.lib, native.handle
+
+    def lm_head(k, s):
+        return lib.kudacuda_lm_head_argmax_bf16(h, p(d_x), 0, p(d_e), p(outs[k][0]), p(outs[k][1]), vocab, 2048,
+                                                 1.0e-6, s.cuda_stream)
+
+    stream.synchronize()
+    assert lib.kudacuda_begin_capture(h, stream.cuda_stream) == 0, native.error()
+    assert lm_head(0, stream) == 0, native.error()
+    assert lib.kudacuda_end_capture(h, stream.cuda_stream) == 0, native.error()
+    try:
+        with torch.cuda.stream(other):
+            torch.cuda._sleep(1_000_000_000)  # keeps the other stream busy (bounded spin)
+        assert lm_head(1, other) == 0, native.error()
+        assert lib.kudacuda_replay_graph(h, stream.cuda_stream) == 1 and "scratch" in native.error()
+        other.synchronize()
+        assert lib.kudacuda_replay_graph(h, stream.cuda_stream) == 0, native.error()
+        stream.synchronize()
+        assert np.array_equal(host(outs[0][0]), host(outs[1][0]))
+        assert int(host(outs[0][1])[0]) == int(host(outs[1][1])[0])
+        with torch.cuda.stream(stream):
+            torch.cuda._sleep(1_000_000_000)
+        assert lib.kudacuda_replay_graph(h, stream.cuda_stream) == 0, native.error()
+        assert lm_head(1, other) == 1 and "scratch" in native.error()
+        stream.synchronize()
+        assert lm_head(1, other) == 0, native.error()
+        other.synchronize()
+    finally:
+        stream.synchronize()
+        other.synchronize()
+        assert lib.kudacuda_reset_graph(h) == 0, native.error()
+
+
 def test_vector_add_and_rmsnorm_plumbing(torch_gpu, native, stream):
     torch = torch_gpu
     a = np.arange(1000, dtype=np.float32)

@@ -349,7 +349,7 @@ enum {
     KUDACUDA_QWEN2_ATTN_PARTIALS,  /* fp32 [kudacuda_gqa_workspace_floats(kv_capacity)] */
     KUDACUDA_QWEN2_ATTN_COUNTERS,  /* uint32 [2] */
     KUDACUDA_QWEN2_LM_BEST,        /* fp32 [kudacuda_lm_head_workspace_floats()] */
-    KUDACUDA_QWEN2_LM_COUNTER,     /* uint32 [1] */
+    KUDACUDA_QWEN2_LM_COUNTER,     /* reserved, unused: may be 0 (keeps the field numbers stable) */
     KUDACUDA_QWEN2_MODEL_FIELDS
 };
 

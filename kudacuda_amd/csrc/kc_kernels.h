@@ -270,7 +270,6 @@ struct LmHeadArgs {
     int64_t vocab = 0;
     uint16_t* logits = nullptr;       // [vocab] bf16 (may be null)
     float* block_best = nullptr;      // [2 * grid] (value, index-as-bits)
-    uint32_t* counter = nullptr;      // zero between calls
     int32_t* argmax_out = nullptr;    // receives the token id (may be null)
     // decode bookkeeping (null for a plain lm_head call): [0] step, [1]
     // prompt length, [2] token capacity, [3] stop token id (< 0: none),

@@ -119,7 +119,7 @@ struct Handle {
     float* gqa_partials = nullptr;
     float* gemm_partials = nullptr;  // kc::kGemmScratchFloats (split-K of the prefill GEMMs)
     float* lm_best = nullptr;
-    uint32_t* counters = nullptr;  // [0..1] attention, [2] lm_head
+    uint32_t* counters = nullptr;  // [0..1] attention tickets
     int32_t* argmax_slot = nullptr;
     // this device's copy of the file-scope `scratch` array (device address)
     unsigned char* static_scratch = nullptr;
@@ -573,7 +573,6 @@ hipError_t model_op(const Model& m, int op, int64_t layer, bool bookkeeping, hip
             a.vocab = m.vocab;
             a.logits = ptr<uint16_t>(G[KUDACUDA_QWEN2_LOGITS]);
             a.block_best = ptr<float>(G[KUDACUDA_QWEN2_LM_BEST]);
-            a.counter = ptr<uint32_t>(G[KUDACUDA_QWEN2_LM_COUNTER]);
             if (bookkeeping) {
                 a.control = ptr<int32_t>(G[KUDACUDA_QWEN2_CONTROL]);
                 a.tokens = ptr<int32_t>(G[KUDACUDA_QWEN2_TOKENS]);
@@ -751,7 +750,6 @@ hipError_t model_prefill(const Model& m, uint8_t* ws, int64_t start, int64_t cou
     a.vocab = m.vocab;
     a.logits = ptr<uint16_t>(G[KUDACUDA_QWEN2_LOGITS]);
     a.block_best = ptr<float>(G[KUDACUDA_QWEN2_LM_BEST]);
-    a.counter = ptr<uint32_t>(G[KUDACUDA_QWEN2_LM_COUNTER]);
     a.control = ptr<int32_t>(G[KUDACUDA_QWEN2_CONTROL]);
     a.tokens = ptr<int32_t>(G[KUDACUDA_QWEN2_TOKENS]);
     return launch_lm_head_argmax(a, stream);
@@ -1363,7 +1361,6 @@ int kudacuda_lm_head_argmax_bf16(void* raw, uint64_t input, uint64_t norm_weight
     a.vocab = vocab;
     a.logits = ptr<uint16_t>(logits);
     a.block_best = h->lm_best;
-    a.counter = h->counters + 2;
     a.argmax_out = ptr<int32_t>(argmax_out);
     if (!claim_scratch(h, symbol, as_stream(stream))) {
         return 1;
@@ -1508,7 +1505,7 @@ void* kudacuda_qwen2_model_create(void* raw, int64_t num_layers, int64_t vocab, 
         }
     }
     for (int i = 0; i < KUDACUDA_QWEN2_MODEL_FIELDS; ++i) {
-        if (model_ptrs[i] == 0 && i != KUDACUDA_QWEN2_LOGITS) {
+        if (model_ptrs[i] == 0 && i != KUDACUDA_QWEN2_LOGITS && i != KUDACUDA_QWEN2_LM_COUNTER) {
             h->set_error("qwen2_model_create: model field " + std::to_string(i) + " is null");
             return nullptr;
         }

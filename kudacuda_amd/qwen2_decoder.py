@@ -95,7 +95,6 @@ class Qwen2Nf4Decoder:
                                          device=device)
             self.attn_counters = t.zeros(2, dtype=t.int32, device=device)
             self.lm_best = t.zeros(int(lib.kudacuda_lm_head_workspace_floats()), dtype=t.float32, device=device)
-            self.lm_counter = t.zeros(1, dtype=t.int32, device=device)
             for layer in self.layers:
                 layer["key_cache"] = t.zeros((cfg.kv_heads, self.kv_capacity, cfg.head_dim), dtype=t.bfloat16,
                                              device=device)
@@ -110,9 +109,10 @@ class Qwen2Nf4Decoder:
             "rope_sin": self.rope_sin, "hidden": self.hidden, "query": self.query, "attn": self.attn,
             "mlp": self.mlp, "logits": self.logits, "tokens": self.tokens, "control": self.control,
             "attn_partials": self.attn_partials, "attn_counters": self.attn_counters, "lm_best": self.lm_best,
-            "lm_counter": self.lm_counter,
+            "lm_counter": None,  # reserved field, unused by the library
         }
-        self.model_table = np.array([model_values[n].data_ptr() for n in QWEN2_MODEL_FIELDS], dtype=np.uint64)
+        self.model_table = np.array([0 if model_values[n] is None else model_values[n].data_ptr()
+                                     for n in QWEN2_MODEL_FIELDS], dtype=np.uint64)
         self.model = lib.kudacuda_qwen2_model_create(
             native.handle, self.num_layers, self.vocab, self.kv_capacity, float(cfg.eps),
             self.layer_table.ctypes.data, self.model_table.ctypes.data,

@@ -141,6 +141,48 @@ def _rel_close(got, want, what, rtol=1e-2, atol=1e-3):
     assert float(err.max()) <= rtol * scale + atol, what
 
 
+def _bf16_ulps_apart(got, want):
+    """Distance in bf16 steps between two arrays of bf16 values (held as
+    fp32): the bit patterns mapped to an order-preserving integer line."""
+
+    def line(x):
+        bits = (np.ascontiguousarray(x, dtype=np.float32).view(np.uint32) >> 16).astype(np.int64)
+        return np.where(bits & 0x8000, -(bits & 0x7FFF), bits)
+
+    return np.abs(line(got) - line(want))
+
+
+def _check_prefill(gpu, ref, layers, count, what):
+    """Layer 0 (identical inputs): at most 0.2 % of the elements more than one
+    bf16 step from the reference (measured: 1 of 6144 and 27 of 25600 differ
+    at all; the largest step counts sit on small values, where the two fp32
+    summation orders differ by a few ulps of the terms, not of the result);
+    every layer within the tensor-scale bound of _rel_close; last-row logits
+    within 0.03 (one to two bf16 steps at their range of ~3); the device's
+    token is the first maximum of its own logits."""
+
+    for li in range(layers):
+        for name in ("key_cache", "value_cache"):
+            got = O.bf16_to_f32(host(gpu.layers[li][name]).reshape(2, -1, 128)[:, :count])
+            want = (ref["kcache"] if name == "key_cache" else ref["vcache"])[li]
+            if li == 0:
+                far = int(np.count_nonzero(_bf16_ulps_apart(got, want) > 1))
+                print(f"{what}: layer 0 {name}: {far} of {got.size} more than one bf16 step apart", flush=True)
+                assert far <= 0.002 * got.size, (what, name, far)
+            _rel_close(got, want, f"layer {li} {name}")
+    got_logits = O.bf16_to_f32(host(gpu.logits))
+    want_logits = O.bf16_to_f32(ref["logits"])
+    err = float(np.abs(got_logits - want_logits).max())
+    top2 = np.sort(want_logits)[-2:]
+    print(f"last-row logits: max |diff| {err:.4g} (range {np.abs(want_logits).max():.3f}, "
+          f"reference top-2 margin {top2[1] - top2[0]:.4g})", flush=True)
+    assert err <= 0.03
+    assert host(gpu.control)[0] == count
+    token = int(host(gpu.tokens)[count])
+    assert token == int(np.argmax(got_logits))  # first maximum, as torch.argmax
+    return err, top2[1] - top2[0], token
+
+
 def test_model_prefill_matches_the_host_restatement(torch_gpu, prefill_pair):
     from kudacuda_amd import synthetic
     from tests._prefill_ref import prefill_reference
@@ -151,22 +193,12 @@ def test_model_prefill_matches_the_host_restatement(torch_gpu, prefill_pair):
     gpu.prefill(prompt)
     gpu.stream.synchronize()
     ref = prefill_reference(cpu, prompt)
-    for li in range(PREFILL_KW["num_layers"]):
-        for name in ("key_cache", "value_cache"):
-            got = O.bf16_to_f32(host(gpu.layers[li][name]).reshape(2, -1, 128)[:, :PROMPT_LEN])
-            want = (ref["kcache"] if name == "key_cache" else ref["vcache"])[li]
-            _rel_close(got, want, f"layer {li} {name}")
-    got_logits = O.bf16_to_f32(host(gpu.logits))
-    want_logits = O.bf16_to_f32(ref["logits"])
-    err = float(np.abs(got_logits - want_logits).max())
-    print(f"last-row logits: max |diff| {err:.4g} (range {np.abs(want_logits).max():.3f})", flush=True)
-    assert err <= 0.05
-    control = host(gpu.control)
-    tokens = host(gpu.tokens)
-    assert control[0] == PROMPT_LEN and tokens[:PROMPT_LEN].tolist() == prompt.tolist()
-    top2 = np.sort(want_logits)[-2:]
-    if top2[1] - top2[0] > 2 * err:  # the greedy token is decided beyond the error
-        assert tokens[PROMPT_LEN] == ref["token"]
+    err, margin, token = _check_prefill(gpu, ref, PREFILL_KW["num_layers"], PROMPT_LEN, "24-token prompt")
+    assert host(gpu.tokens)[:PROMPT_LEN].tolist() == prompt.tolist()
+    # this seed's reference margin (0.031) is two bf16 steps: the token equals
+    # the reference's wherever the logits' error leaves it decided
+    if margin > 2 * err:
+        assert token == ref["token"]
 
 
 LONG_KW = dict(num_layers=2, vocab=4096, kv_capacity=128, token_capacity=128)
@@ -190,20 +222,9 @@ def test_model_prefill_of_a_multi_chunk_prompt(torch_gpu, native):
         gpu.prefill(prompt)
         gpu.stream.synchronize()
         ref = prefill_reference(cpu, prompt)
-        for li in range(LONG_KW["num_layers"]):
-            for name in ("key_cache", "value_cache"):
-                got = O.bf16_to_f32(host(gpu.layers[li][name]).reshape(2, -1, 128)[:, :LONG_PROMPT])
-                want = (ref["kcache"] if name == "key_cache" else ref["vcache"])[li]
-                _rel_close(got, want, f"layer {li} {name}")
-        got_logits = O.bf16_to_f32(host(gpu.logits))
-        want_logits = O.bf16_to_f32(ref["logits"])
-        err = float(np.abs(got_logits - want_logits).max())
-        print(f"last-row logits: max |diff| {err:.4g}", flush=True)
-        assert err <= 0.05
-        assert host(gpu.control)[0] == LONG_PROMPT
-        top2 = np.sort(want_logits)[-2:]
-        if top2[1] - top2[0] > 2 * err:
-            assert host(gpu.tokens)[LONG_PROMPT] == ref["token"]
+        err, margin, token = _check_prefill(gpu, ref, LONG_KW["num_layers"], LONG_PROMPT, "100-token prompt")
+        assert margin > 2 * err  # this seed's reference margin is 0.22: the token is decided
+        assert token == ref["token"]
     finally:
         gpu.close()
 

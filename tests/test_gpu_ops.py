@@ -425,8 +425,35 @@ def test_lm_head_argmax(torch_gpu, native, stream, vocab, with_norm):
     assert tok == int(np.argmax(lf))  # first maximum, as torch.argmax
 
 
+def test_lm_head_argmax_ties_across_waves_and_blocks(torch_gpu, native, stream):
+    """One maximal row planted at several indices: in one wave's ring (rows
+    3072 apart at 768 blocks of 4 waves), in other blocks and at the last
+    row.  Their logits are bit-equal, so the lowest index must win through
+    the wave, the block and the one-block winner reduction alike."""
+    torch = torch_gpu
+    vocab = 151936
+    x = synthetic.f32_to_bf16_bits(synthetic.normal(SEED, (14,), (2048,), 1.0))
+    emb = synthetic.embedding_bits(SEED, vocab=vocab)
+    # a row along x, well above every random row's logit
+    xf = O.bf16_to_f32(x).astype(np.float64)
+    hot = synthetic.f32_to_bf16_bits((0.05 * xf / np.sqrt(np.mean(xf * xf))).astype(np.float32))
+    planted = [7, 7 + 3072, 40001, 98765, vocab - 1]
+    emb[planted] = hot
+    d_x, d_e = dev(torch, x), dev(torch, emb)
+    logits = empty(torch, vocab, "u16")
+    arg = empty(torch, 1, "i32")
+    native.call("kudacuda_lm_head_argmax_bf16", p(d_x), 0, p(d_e), p(logits), p(arg), vocab, 2048, 1.0e-6,
+                stream.cuda_stream)
+    stream.synchronize()
+    tok, elog = O.lm_head_argmax(x, None, 1.0e-6, emb)
+    lf = O.bf16_to_f32(elog)
+    assert tok == 7 and np.all(lf[planted] == lf.max()) and np.count_nonzero(lf == lf.max()) == len(planted)
+    assert np.array_equal(host(logits), elog)
+    assert int(host(arg)[0]) == 7
+
+
 def test_handle_scratch_is_refused_to_a_second_busy_stream(torch_gpu, native, stream):
-    """The handle's scratch (here lm_head's block winners and ticket) serves
+    """The handle's scratch (here lm_head's block winners) serves
     one stream at a time: a call on another stream is refused while the last
     user's stream still has work queued, and accepted once it is idle."""
     torch = torch_gpu

@@ -73,6 +73,7 @@ SIGNATURES: dict[str, tuple[list[Any], Any]] = {
     "kudacuda_qwen2_model_step": ([_vp, _u64], _i),
     "kudacuda_qwen2_model_capture": ([_vp, _u64], _i),
     "kudacuda_qwen2_model_replay": ([_vp, _i64, _u64], _i),
+    "kudacuda_qwen2_model_set_position": ([_vp, _i64], _i),
     "kudacuda_qwen2_model_time_op": ([_vp, _i64, _i64, _u64, ctypes.POINTER(_f)], _i),
     "kudacuda_qwen2_prefill_workspace_bytes": ([_i64], _i64),
     "kudacuda_qwen2_model_prefill": ([_vp, _u64, _i64, _i64, _i64, _u64], _i),

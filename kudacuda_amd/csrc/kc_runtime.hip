@@ -454,9 +454,20 @@ struct Model {
     std::array<uint64_t, KUDACUDA_QWEN2_MODEL_FIELDS> g{};
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    // the step captured for long caches (attention merged by the merge
+    // kernel, o_proj a plain GEMV), when the plan can leave more splits than
+    // o_proj merges; chosen per step by host_step
+    hipGraphExec_t exec_long = nullptr;
+    // the step (control[0]) the next launch runs at, as far as the host
+    // knows (-1: unknown); only picks between the two step forms, which
+    // compute the same results
+    int64_t host_step = -1;
     ~Model() {
         if (exec != nullptr) {
             (void)hipGraphExecDestroy(exec);
+        }
+        if (exec_long != nullptr) {
+            (void)hipGraphExecDestroy(exec_long);
         }
         if (graph != nullptr) {
             (void)hipGraphDestroy(graph);
@@ -464,7 +475,14 @@ struct Model {
     }
 };
 
-hipError_t model_op(const Model& m, int op, int64_t layer, bool bookkeeping, hipStream_t stream) {
+// long_ctx: the step form for caches whose split count exceeds what o_proj
+// merges -- attention's partials all go to gqa_merge_kernel (one more launch,
+// parallel over heads and dims) and o_proj reads the merged vector as a plain
+// GEMV; the short form leaves up to kGqaMaxDefer splits to o_proj and merges
+// more by the attention kernel's ticket, with no merge launch in the graph.
+// Both forms merge by the same rule in the same order: identical results.
+hipError_t model_op(const Model& m, int op, int64_t layer, bool bookkeeping, hipStream_t stream,
+                    bool long_ctx = false) {
     const auto& L = m.layers[static_cast<size_t>(layer)];
     const auto& G = m.g;
     switch (op) {
@@ -512,10 +530,15 @@ hipError_t model_op(const Model& m, int op, int64_t layer, bool bookkeeping, hip
             a.kv_len_device = ptr<const int32_t>(G[KUDACUDA_QWEN2_CONTROL]);
             a.kv_len_offset = 1;
             set_gqa_plan(a, m.capacity, kGqaStepSplits);
-            a.defer_max = model_defer(a.max_splits);  // o_proj merges these
-            // the rest by ticket: a merge kernel would be one more graph node
-            // per layer even at the lengths that never need it
-            a.ticket_max = 32;
+            if (long_ctx) {
+                a.defer_max = 0;   // gqa_merge_kernel merges every split count above one
+                a.ticket_max = 1;
+            } else {
+                a.defer_max = model_defer(a.max_splits);  // o_proj merges these
+                // the rest by ticket: a merge kernel would be one more graph
+                // node per layer even at the lengths that never need it
+                a.ticket_max = 32;
+            }
             a.qk_scale_log2 = static_cast<float>(1.0 / std::sqrt(128.0)) * kLog2e;
             return launch_gqa_decode(Act::kBf16, a, stream);
         }
@@ -527,6 +550,9 @@ hipError_t model_op(const Model& m, int op, int64_t layer, bool bookkeeping, hip
             a.out[0] = ptr<uint16_t>(G[KUDACUDA_QWEN2_HIDDEN]);
             a.residual = ptr<const uint16_t>(G[KUDACUDA_QWEN2_HIDDEN]);
             a.rows[0] = 2048;
+            if (long_ctx) {
+                return launch_nf4_rows2048(RowMode::kGemv, Act::kBf16, a, stream);  // x merged by op 1
+            }
             // attention output: merged here from the partials op 1 left
             GqaArgs plan;
             set_gqa_plan(plan, m.capacity, kGqaStepSplits);
@@ -755,10 +781,25 @@ hipError_t model_prefill(const Model& m, uint8_t* ws, int64_t start, int64_t cou
     return launch_lm_head_argmax(a, stream);
 }
 
-hipError_t model_step(const Model& m, hipStream_t stream) {
+// Whether the step at `step` (kv_len step + 1) needs more splits than o_proj
+// merges, so that the long form is the faster one.
+bool long_step(const Model& m, int64_t step) {
+    if (step < 0) {
+        return false;
+    }
+    GqaArgs plan;
+    set_gqa_plan(plan, m.capacity, kGqaStepSplits);
+    const int64_t kv_len = step + 1 < m.capacity ? step + 1 : m.capacity;
+    return gqa_split_count(kv_len, plan.split_cap) > model_defer(plan.max_splits);
+}
+
+// Whether a cache of the model's capacity can reach the long form at all.
+bool long_form_possible(const Model& m) { return long_step(m, m.capacity - 1); }
+
+hipError_t model_step(const Model& m, hipStream_t stream, bool long_ctx = false) {
     for (int64_t layer = 0; layer < m.num_layers; ++layer) {
         for (int op = 0; op < 5; ++op) {
-            const hipError_t status = model_op(m, op, layer, true, stream);
+            const hipError_t status = model_op(m, op, layer, true, stream, long_ctx);
             if (status != hipSuccess) {
                 return status;
             }
@@ -1539,7 +1580,11 @@ int kudacuda_qwen2_model_step(void* raw_model, uint64_t stream) {
     if (m == nullptr) {
         return 1;
     }
-    return finish(m->handle, "qwen2_model_step", kc::model_step(*m, as_stream(stream)));
+    const hipError_t status = kc::model_step(*m, as_stream(stream), kc::long_step(*m, m->host_step));
+    if (status == hipSuccess && m->host_step >= 0) {
+        ++m->host_step;
+    }
+    return finish(m->handle, "qwen2_model_step", status);
 }
 
 int64_t kudacuda_qwen2_prefill_workspace_bytes(int64_t tokens) {
@@ -1565,7 +1610,11 @@ int kudacuda_qwen2_model_prefill(void* raw_model, uint64_t workspace, int64_t wo
                      "kudacuda_qwen2_prefill_workspace_bytes(count) bytes");
         return 1;
     }
-    return finish(h, symbol, kc::model_prefill(*m, ptr<uint8_t>(workspace), start, count, as_stream(stream)));
+    const hipError_t status = kc::model_prefill(*m, ptr<uint8_t>(workspace), start, count, as_stream(stream));
+    if (status == hipSuccess) {
+        m->host_step = start + count;  // where the prefill leaves control[0]
+    }
+    return finish(h, symbol, status);
 }
 
 int kudacuda_qwen2_model_capture(void* raw_model, uint64_t stream) {
@@ -1574,33 +1623,49 @@ int kudacuda_qwen2_model_capture(void* raw_model, uint64_t stream) {
         return 1;
     }
     Handle* h = m->handle;
-    if (m->exec != nullptr) {
-        (void)hipGraphExecDestroy(m->exec);
-        m->exec = nullptr;
+    for (hipGraphExec_t* e : {&m->exec, &m->exec_long}) {
+        if (*e != nullptr) {
+            (void)hipGraphExecDestroy(*e);
+            *e = nullptr;
+        }
     }
     hipStream_t s = as_stream(stream);
-    hipError_t status = hipStreamBeginCapture(s, hipStreamCaptureModeGlobal);
-    if (status != hipSuccess) {
-        return finish(h, "hipStreamBeginCapture", status);
-    }
-    const hipError_t launch_status = kc::model_step(*m, s);
-    hipGraph_t graph = nullptr;
-    status = hipStreamEndCapture(s, &graph);
-    if (launch_status != hipSuccess) {
-        if (graph != nullptr) {
-            (void)hipGraphDestroy(graph);
+    // the short form always; the long form when this cache can need it
+    const bool forms[2] = {false, true};
+    for (const bool long_ctx : forms) {
+        if (long_ctx && !kc::long_form_possible(*m)) {
+            break;
         }
-        return finish(h, "qwen2_model_capture(step)", launch_status);
+        hipGraphExec_t* dst = long_ctx ? &m->exec_long : &m->exec;
+        hipError_t status = hipStreamBeginCapture(s, hipStreamCaptureModeGlobal);
+        if (status != hipSuccess) {
+            return finish(h, "hipStreamBeginCapture", status);
+        }
+        const hipError_t launch_status = kc::model_step(*m, s, long_ctx);
+        hipGraph_t graph = nullptr;
+        status = hipStreamEndCapture(s, &graph);
+        if (launch_status != hipSuccess) {
+            if (graph != nullptr) {
+                (void)hipGraphDestroy(graph);
+            }
+            return finish(h, "qwen2_model_capture(step)", launch_status);
+        }
+        if (status != hipSuccess) {
+            return finish(h, "hipStreamEndCapture", status);
+        }
+        status = hipGraphInstantiate(dst, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        if (status != hipSuccess) {
+            *dst = nullptr;
+            if (long_ctx && m->exec != nullptr) {
+                (void)hipGraphExecDestroy(m->exec);  // all or nothing
+                m->exec = nullptr;
+            }
+            return finish(h, "hipGraphInstantiate", status);
+        }
     }
-    if (status != hipSuccess) {
-        return finish(h, "hipStreamEndCapture", status);
-    }
-    status = hipGraphInstantiate(&m->exec, graph, nullptr, nullptr, 0);
-    (void)hipGraphDestroy(graph);
-    if (status != hipSuccess) {
-        m->exec = nullptr;
-    }
-    return finish(h, "hipGraphInstantiate", status);
+    h->last_error.clear();
+    return 0;
 }
 
 int kudacuda_qwen2_model_replay(void* raw_model, int64_t steps, uint64_t stream) {
@@ -1613,11 +1678,25 @@ int kudacuda_qwen2_model_replay(void* raw_model, int64_t steps, uint64_t stream)
         return 1;
     }
     for (int64_t i = 0; i < steps; ++i) {
-        const hipError_t status = hipGraphLaunch(m->exec, as_stream(stream));
+        const bool long_ctx = m->exec_long != nullptr && kc::long_step(*m, m->host_step);
+        const hipError_t status = hipGraphLaunch(long_ctx ? m->exec_long : m->exec, as_stream(stream));
         if (status != hipSuccess) {
             return finish(m->handle, "hipGraphLaunch", status);
         }
+        if (m->host_step >= 0) {
+            ++m->host_step;
+        }
     }
+    m->handle->last_error.clear();
+    return 0;
+}
+
+int kudacuda_qwen2_model_set_position(void* raw_model, int64_t step) {
+    auto* m = reinterpret_cast<kc::Model*>(raw_model);
+    if (m == nullptr) {
+        return 1;
+    }
+    m->host_step = step < 0 ? -1 : step;
     m->handle->last_error.clear();
     return 0;
 }

@@ -168,6 +168,7 @@ class Qwen2Nf4Decoder:
             self.control.copy_(t.tensor([start_step, prompt.size, self.token_capacity, stop, 0, 0, 0, 0],
                                         dtype=t.int32))
         self.stream.synchronize()
+        self._set_position(start_step)
 
     def stopped_at(self) -> int | None:
         """Position of the stop token in the token array, or None while running."""
@@ -180,6 +181,13 @@ class Qwen2Nf4Decoder:
         with t.cuda.stream(self.stream):
             self.control[0:1].copy_(t.tensor([int(step)], dtype=t.int32))
         self.stream.synchronize()
+        self._set_position(step)
+
+    def _set_position(self, step: int) -> None:
+        # tells the library which step runs next, so that replays pick the
+        # faster form of the step for the cache length (results do not depend on it)
+        self.native.check(self.native.lib.kudacuda_qwen2_model_set_position(self.model, int(step)),
+                          "kudacuda_qwen2_model_set_position")
 
     def step(self) -> None:
         self.native.check(self.native.lib.kudacuda_qwen2_model_step(self.model, self.stream.cuda_stream),

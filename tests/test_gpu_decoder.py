@@ -151,14 +151,20 @@ def test_long_context_decode_matches_oracle(torch_gpu, native, prompt_len, new, 
         gpu.close()
 
 
-@pytest.mark.parametrize("start,capacity", [(2100, 4096), (4200, 8192)])
-def test_decode_from_a_seeded_long_cache_matches_oracle(torch_gpu, native, start, capacity):
+@pytest.mark.parametrize("start,capacity,mode", [
+    (2100, 4096, "eager"), (4200, 8192, "eager"),
+    (700, 1024, "graph"), (700, 1024, "graph, position unknown"), (189, 1024, "graph"),
+])
+def test_decode_from_a_seeded_long_cache_matches_oracle(torch_gpu, native, start, capacity, mode):
     # Longer splits inside the decode step: both models get the same random
     # cache rows 0..start-1 and decode from position start.  At 2100+ tokens
     # the step's plan makes 22 splits of three 32-token rounds, at 4200 of an
-    # 8192-row cache 27 splits of five rounds; both are merged by the
-    # attention kernel's ticket (the step's plan never exceeds 32 splits, so
-    # its graph holds no merge kernel).
+    # 8192-row cache 27 splits of five rounds, at 700 22 one-round splits.
+    # Past 6 splits (192 cached tokens) the step runs in its long-cache form
+    # (gqa_merge_kernel merges the splits, o_proj is a plain GEMV) when the
+    # library knows the position, in the short form (the attention kernel's
+    # ticket merges them) when it does not; from 189 the steps cross that
+    # boundary (kv_len 190 .. 195).  Every form must equal the oracle.
     torch = torch_gpu
     new = 6
     kw = dict(num_layers=2, vocab=4096, kv_capacity=capacity, token_capacity=capacity)
@@ -179,8 +185,16 @@ def test_decode_from_a_seeded_long_cache_matches_oracle(torch_gpu, native, start
         prompt = synthetic.prompt_ids(SEED + 4, start + 1, 4096)
         gpu.reset(prompt, start_step=start)
         cpu.reset(prompt, start_step=start)
+        if mode != "eager":
+            gpu.capture()
+        if mode == "graph, position unknown":
+            gpu._set_position(-1)
+        print(f"seeded cache: start {start}, capacity {capacity}, {mode}", flush=True)
         for step in range(new):
-            gpu.step()
+            if mode == "eager":
+                gpu.step()
+            else:
+                gpu.replay(1)
             gpu.stream.synchronize()
             cpu.step()
             ctx = f"position {start + step}"

@@ -361,22 +361,22 @@ KUDACUDA_API void* kudacuda_qwen2_model_create(void* handle, int64_t num_layers,
                                                const uint64_t* model_ptrs);
 /* Launch one decode step on `stream` (eager). */
 KUDACUDA_API int kudacuda_qwen2_model_step(void* model, uint64_t stream);
-/* Capture one decode step into the model's own hipGraph (replaces any
- * previous one) and instantiate it; the step is not executed.  When the cache
- * can hold more tokens than the short-context plan merges inside o_proj (more
- * than 6 splits of 32 tokens per KV head), a second form of the step is
- * captured too, for long caches (attention merged by its own kernel, o_proj
- * as a plain GEMV). */
+/* Capture one decode step into the model's own hipGraphs (replaces any
+ * previous ones) and instantiate them; the step is not executed.  The step
+ * is captured in one form per attention split count o_proj can merge (1..6
+ * splits of 32 cached tokens per KV head, o_proj requesting exactly that
+ * many) and, when the cache can hold more, in a form for long caches
+ * (attention merged by its own kernel, o_proj as a plain GEMV). */
 KUDACUDA_API int kudacuda_qwen2_model_capture(void* model, uint64_t stream);
 /* Replay the captured step `steps` times back to back on `stream`.  Each
- * replay (and each eager step) takes the form that is faster at the step the
- * host believes it runs at (kudacuda_qwen2_model_set_position, advanced by
- * one per step; set by model_prefill); both forms compute identical results,
- * so a wrong or unknown position costs time only. */
+ * replay (and each eager step) takes the form made for the step the host
+ * believes it runs at (kudacuda_qwen2_model_set_position, advanced by one
+ * per step; set by model_prefill); every form computes identical results at
+ * any length, so a wrong or unknown position costs time only. */
 KUDACUDA_API int kudacuda_qwen2_model_replay(void* model, int64_t steps, uint64_t stream);
 /* NEW (no reference counterpart) -- the step value (control[0]) the next
- * step or replay runs at, or -1 for unknown (then the short-context form
- * runs).  Call it whenever the caller writes control[0] itself. */
+ * step or replay runs at, or -1 for unknown (then the 6-split form runs).
+ * Call it whenever the caller writes control[0] itself. */
 KUDACUDA_API int kudacuda_qwen2_model_set_position(void* model, int64_t step);
 /* Time one kernel of the step in isolation: op 0 = qkv+rope, 1 = attention,
  * 2 = o_proj, 3 = gate/up, 4 = down, 5 = lm_head; `iters` (1..4096) launches

@@ -250,8 +250,8 @@ struct RowsHot {
 // issue order, so the norm waits only for the small vectors while the rows
 // stream in, and each task's dot waits only for its own rows.
 //
-// ATTN (kGemv only): x is the output of split-KV attention.  When the
-// partials were left unmerged (split count <= attn.defer_max), thread t
+// ATTN > 0 (kGemv only): x is the output of split-KV attention.  When the
+// partials were left unmerged (split count <= attn.defer_max = ATTN), thread t
 // merges head t/16, dims 8(t%16)..+7: M = max of the split maxima, weights
 // exp2(m_s - M), sum and acc accumulated in split order, x = T(acc / sum) --
 // the attention kernel's own merge -- into LDS before the block barrier.
@@ -261,12 +261,13 @@ struct RowsHot {
 // The six leading pointer arguments are preloaded into SGPRs at wave launch
 // (the fields the first, longest loads need; RowsHot maps them per mode) and
 // stand for the same fields of `args`.
-template <typename T, RowMode MODE, int TPW, bool ATTN = false, int NTH = kRowsThreads>
+template <typename T, RowMode MODE, int TPW, int ATTN = 0, int NTH = kRowsThreads>
 __global__ __launch_bounds__(NTH) void nf4_rows2048_kernel(const void* h0, const void* h1, const void* h2,
                                                            const void* h3, const void* h4, const void* h5,
                                                            Nf4RowsArgs args, int64_t ntasks) {
     Nf4RowsArgs a = args;
     RowsHot<MODE>::apply(a, h0, h1, h2, h3, h4, h5);
+    static_assert(ATTN >= 0 && ATTN <= kGqaMaxDefer, "deferred split slots");
     static_assert(!ATTN || MODE == RowMode::kGemv, "attention merge feeds the GEMV only");
     static_assert(!ATTN || kRowsThreads * 8 == 2048, "one thread per 8 merged outputs");
     // kQkv / kQkvRope / kSwiGlu: the block shares the RMSNorm (waves 0..3 each
@@ -307,17 +308,19 @@ __global__ __launch_bounds__(NTH) void nf4_rows2048_kernel(const void* h0, const
     }
     const bool has_gamma = !ATTN && a.gamma != nullptr;
     int64_t attn_len = 0;
-    float2 pml[ATTN ? kGqaMaxDefer : 1];
-    float2 pv[ATTN ? kGqaMaxDefer : 1][4];
-    if constexpr (ATTN) {
-        // splits past the plan's count re-read split 0 (loads unconditional)
+    // one slot per split the attention may defer (ATTN = attn.defer_max)
+    float2 pml[ATTN ? ATTN : 1];
+    float2 pv[ATTN ? ATTN : 1][4];
+    if constexpr (ATTN > 0) {
+        // every slot is requested (loads unconditional); slots past the
+        // split count at this length are read, never used
         attn_len = static_cast<int64_t>(*a.attn.kv_len_device) + a.attn.kv_len_offset;
         const float* src = a.attn.partials + static_cast<int64_t>(threadIdx.x >> 4) * a.attn.max_splits *
                                                  kGqaPartialStride;
         const int d0 = 8 * (threadIdx.x & 15);
 #pragma unroll
-        for (int x = 0; x < kGqaMaxDefer; ++x) {
-            const float* row = src + (x < a.attn.defer_max ? x : 0) * kGqaPartialStride;
+        for (int x = 0; x < ATTN; ++x) {
+            const float* row = src + x * kGqaPartialStride;
             pml[x] = *reinterpret_cast<const float2*>(row);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -379,14 +382,14 @@ __global__ __launch_bounds__(NTH) void nf4_rows2048_kernel(const void* h0, const
     __builtin_amdgcn_sched_barrier(0);
 
     bool merged = false;
-    if constexpr (ATTN) {
+    if constexpr (ATTN > 0) {
         const int64_t L = attn_len < 0 ? 0 : (attn_len > a.attn.capacity ? a.attn.capacity : attn_len);
         const int64_t nsplit = gqa_split_count(L, a.attn.split_cap);
         merged = nsplit >= 1 && nsplit <= a.attn.defer_max;
         if (merged) {
             float M = -__builtin_huge_valf();
 #pragma unroll
-            for (int x = 0; x < kGqaMaxDefer; ++x) {
+            for (int x = 0; x < ATTN; ++x) {
                 M = x < nsplit ? fmaxf(M, pml[x].x) : M;
             }
             // the 16 threads of a head form one DPP row: lane x of the row
@@ -394,17 +397,17 @@ __global__ __launch_bounds__(NTH) void nf4_rows2048_kernel(const void* h0, const
             const int ri = threadIdx.x & 15;
             float mi = pml[0].x;
 #pragma unroll
-            for (int x = 1; x < kGqaMaxDefer; ++x) {
+            for (int x = 1; x < ATTN; ++x) {
                 mi = ri == x ? pml[x].x : mi;
             }
             const float wi = exp2_fixed(mi - M);
-            float wx[kGqaMaxDefer];
-            static_assert(kGqaMaxDefer <= 16, "one broadcast per deferred split, within a 16-lane row");
-            row_bcast_all(wi, wx, std::make_integer_sequence<int, kGqaMaxDefer>{});
+            float wx[ATTN];
+            static_assert(ATTN <= 16, "one broadcast per deferred split, within a 16-lane row");
+            row_bcast_all(wi, wx, std::make_integer_sequence<int, ATTN>{});
             float lt = 0.0f;
             float o[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int x = 0; x < kGqaMaxDefer; ++x) {
+            for (int x = 0; x < ATTN; ++x) {
                 if (x < nsplit) {
                     const float w = wx[x];
                     lt = fmaf(pml[x].y, w, lt);
@@ -743,9 +746,24 @@ hipError_t launch_rows_tpw(const Nf4RowsArgs& a, int64_t ntasks, int64_t blocks,
     const dim3 grid(static_cast<unsigned>(blocks));
     if constexpr (MODE == RowMode::kGemv && TPW == 1) {
         if (a.attn.partials != nullptr) {
-            hipLaunchKernelGGL((nf4_rows2048_kernel<T, MODE, TPW, true>), grid, dim3(kRowsThreads), 0, stream, h[0],
-                               h[1], h[2], h[3], h[4], h[5], a, ntasks);
-            return hipGetLastError();
+            // one instantiation per deferral slot count (1..kGqaMaxDefer, checked by the caller)
+            static_assert(kGqaMaxDefer == 6, "one case per slot count");
+            switch (a.attn.defer_max) {
+#define KC_ATTN_CASE(K)                                                                                      \
+    case K:                                                                                                  \
+        hipLaunchKernelGGL((nf4_rows2048_kernel<T, MODE, TPW, K>), grid, dim3(kRowsThreads), 0, stream, h[0], \
+                           h[1], h[2], h[3], h[4], h[5], a, ntasks);                                         \
+        return hipGetLastError();
+                KC_ATTN_CASE(1)
+                KC_ATTN_CASE(2)
+                KC_ATTN_CASE(3)
+                KC_ATTN_CASE(4)
+                KC_ATTN_CASE(5)
+                KC_ATTN_CASE(6)
+#undef KC_ATTN_CASE
+                default:
+                    return hipErrorInvalidValue;
+            }
         }
     }
     if constexpr (MODE == RowMode::kSwiGlu) {

@@ -453,21 +453,18 @@ struct Model {
     std::vector<std::array<uint64_t, KUDACUDA_QWEN2_LAYER_FIELDS>> layers;
     std::array<uint64_t, KUDACUDA_QWEN2_MODEL_FIELDS> g{};
     hipGraph_t graph = nullptr;
-    hipGraphExec_t exec = nullptr;
-    // the step captured for long caches (attention merged by the merge
-    // kernel, o_proj a plain GEMV), when the plan can leave more splits than
-    // o_proj merges; chosen per step by host_step
-    hipGraphExec_t exec_long = nullptr;
+    // the captured step in each of its forms (index = form, see model_op);
+    // forms 1 .. step_defer_cap always, form 0 when the cache can need it
+    std::array<hipGraphExec_t, kGqaMaxDefer + 1> execs{};
     // the step (control[0]) the next launch runs at, as far as the host
-    // knows (-1: unknown); only picks between the two step forms, which
-    // compute the same results
+    // knows (-1: unknown); only picks among the step forms, which compute
+    // the same results
     int64_t host_step = -1;
     ~Model() {
-        if (exec != nullptr) {
-            (void)hipGraphExecDestroy(exec);
-        }
-        if (exec_long != nullptr) {
-            (void)hipGraphExecDestroy(exec_long);
+        for (hipGraphExec_t e : execs) {
+            if (e != nullptr) {
+                (void)hipGraphExecDestroy(e);
+            }
         }
         if (graph != nullptr) {
             (void)hipGraphDestroy(graph);
@@ -475,14 +472,25 @@ struct Model {
     }
 };
 
-// long_ctx: the step form for caches whose split count exceeds what o_proj
-// merges -- attention's partials all go to gqa_merge_kernel (one more launch,
-// parallel over heads and dims) and o_proj reads the merged vector as a plain
-// GEMV; the short form leaves up to kGqaMaxDefer splits to o_proj and merges
-// more by the attention kernel's ticket, with no merge launch in the graph.
-// Both forms merge by the same rule in the same order: identical results.
+// The step's deferral cap: splits attention leaves for o_proj to merge.
+int64_t step_defer_cap(const Model& m) {
+    GqaArgs plan;
+    set_gqa_plan(plan, m.capacity, kGqaStepSplits);
+    return model_defer(plan.max_splits);
+}
+
+// form (ops 1 and 2 only): k = 1 .. step_defer_cap -- attention leaves up to
+// k splits to o_proj, whose merge prologue requests exactly k split slots,
+// and merges more by its own ticket (no merge launch in the graph); -1: k =
+// the cap; 0 -- the form for caches whose split count exceeds the cap:
+// attention's partials all go to gqa_merge_kernel (one more launch, parallel
+// over heads and dims) and o_proj reads the merged vector as a plain GEMV.
+// Every form merges by the same rule in the same order: identical results at
+// any length, only the time differs.
 hipError_t model_op(const Model& m, int op, int64_t layer, bool bookkeeping, hipStream_t stream,
-                    bool long_ctx = false) {
+                    int form = -1) {
+    const bool long_ctx = form == 0;
+    const int64_t defer = form < 0 || form > step_defer_cap(m) ? step_defer_cap(m) : form;
     const auto& L = m.layers[static_cast<size_t>(layer)];
     const auto& G = m.g;
     switch (op) {
@@ -534,7 +542,7 @@ hipError_t model_op(const Model& m, int op, int64_t layer, bool bookkeeping, hip
                 a.defer_max = 0;   // gqa_merge_kernel merges every split count above one
                 a.ticket_max = 1;
             } else {
-                a.defer_max = model_defer(a.max_splits);  // o_proj merges these
+                a.defer_max = defer;  // o_proj merges these
                 // the rest by ticket: a merge kernel would be one more graph
                 // node per layer even at the lengths that never need it
                 a.ticket_max = 32;
@@ -563,7 +571,7 @@ hipError_t model_op(const Model& m, int op, int64_t layer, bool bookkeeping, hip
             a.attn.capacity = plan.capacity;
             a.attn.split_cap = plan.split_cap;
             a.attn.max_splits = plan.max_splits;
-            a.attn.defer_max = model_defer(plan.max_splits);
+            a.attn.defer_max = defer;
             return launch_nf4_rows2048(RowMode::kGemv, Act::kBf16, a, stream);
         }
         case 3: {
@@ -781,25 +789,28 @@ hipError_t model_prefill(const Model& m, uint8_t* ws, int64_t start, int64_t cou
     return launch_lm_head_argmax(a, stream);
 }
 
-// Whether the step at `step` (kv_len step + 1) needs more splits than o_proj
-// merges, so that the long form is the faster one.
-bool long_step(const Model& m, int64_t step) {
+// The fastest form for the step at `step` (kv_len step + 1): the split
+// count itself while o_proj merges it, form 0 past the cap, the cap when the
+// step is unknown.
+int step_form(const Model& m, int64_t step) {
+    const int64_t cap = step_defer_cap(m);
     if (step < 0) {
-        return false;
+        return static_cast<int>(cap);
     }
     GqaArgs plan;
     set_gqa_plan(plan, m.capacity, kGqaStepSplits);
     const int64_t kv_len = step + 1 < m.capacity ? step + 1 : m.capacity;
-    return gqa_split_count(kv_len, plan.split_cap) > model_defer(plan.max_splits);
+    const int64_t nsplit = gqa_split_count(kv_len, plan.split_cap);
+    return nsplit > cap ? 0 : static_cast<int>(nsplit < 1 ? 1 : nsplit);
 }
 
-// Whether a cache of the model's capacity can reach the long form at all.
-bool long_form_possible(const Model& m) { return long_step(m, m.capacity - 1); }
+// Whether a cache of the model's capacity can need form 0 at all.
+bool long_form_possible(const Model& m) { return step_form(m, m.capacity - 1) == 0; }
 
-hipError_t model_step(const Model& m, hipStream_t stream, bool long_ctx = false) {
+hipError_t model_step(const Model& m, hipStream_t stream, int form = -1) {
     for (int64_t layer = 0; layer < m.num_layers; ++layer) {
         for (int op = 0; op < 5; ++op) {
-            const hipError_t status = model_op(m, op, layer, true, stream, long_ctx);
+            const hipError_t status = model_op(m, op, layer, true, stream, form);
             if (status != hipSuccess) {
                 return status;
             }
@@ -1580,7 +1591,7 @@ int kudacuda_qwen2_model_step(void* raw_model, uint64_t stream) {
     if (m == nullptr) {
         return 1;
     }
-    const hipError_t status = kc::model_step(*m, as_stream(stream), kc::long_step(*m, m->host_step));
+    const hipError_t status = kc::model_step(*m, as_stream(stream), kc::step_form(*m, m->host_step));
     if (status == hipSuccess && m->host_step >= 0) {
         ++m->host_step;
     }
@@ -1623,44 +1634,44 @@ int kudacuda_qwen2_model_capture(void* raw_model, uint64_t stream) {
         return 1;
     }
     Handle* h = m->handle;
-    for (hipGraphExec_t* e : {&m->exec, &m->exec_long}) {
-        if (*e != nullptr) {
-            (void)hipGraphExecDestroy(*e);
-            *e = nullptr;
+    auto drop_all = [m]() {
+        for (hipGraphExec_t& e : m->execs) {
+            if (e != nullptr) {
+                (void)hipGraphExecDestroy(e);
+                e = nullptr;
+            }
         }
-    }
+    };
+    drop_all();
     hipStream_t s = as_stream(stream);
-    // the short form always; the long form when this cache can need it
-    const bool forms[2] = {false, true};
-    for (const bool long_ctx : forms) {
-        if (long_ctx && !kc::long_form_possible(*m)) {
-            break;
-        }
-        hipGraphExec_t* dst = long_ctx ? &m->exec_long : &m->exec;
+    // forms 1 .. cap always (the split count a step can leave to o_proj),
+    // form 0 when this cache can exceed the cap
+    const int cap = static_cast<int>(kc::step_defer_cap(*m));
+    for (int form = kc::long_form_possible(*m) ? 0 : 1; form <= cap; ++form) {
         hipError_t status = hipStreamBeginCapture(s, hipStreamCaptureModeGlobal);
         if (status != hipSuccess) {
+            drop_all();
             return finish(h, "hipStreamBeginCapture", status);
         }
-        const hipError_t launch_status = kc::model_step(*m, s, long_ctx);
+        const hipError_t launch_status = kc::model_step(*m, s, form);
         hipGraph_t graph = nullptr;
         status = hipStreamEndCapture(s, &graph);
         if (launch_status != hipSuccess) {
             if (graph != nullptr) {
                 (void)hipGraphDestroy(graph);
             }
+            drop_all();
             return finish(h, "qwen2_model_capture(step)", launch_status);
         }
         if (status != hipSuccess) {
+            drop_all();
             return finish(h, "hipStreamEndCapture", status);
         }
-        status = hipGraphInstantiate(dst, graph, nullptr, nullptr, 0);
+        status = hipGraphInstantiate(&m->execs[static_cast<size_t>(form)], graph, nullptr, nullptr, 0);
         (void)hipGraphDestroy(graph);
         if (status != hipSuccess) {
-            *dst = nullptr;
-            if (long_ctx && m->exec != nullptr) {
-                (void)hipGraphExecDestroy(m->exec);  // all or nothing
-                m->exec = nullptr;
-            }
+            m->execs[static_cast<size_t>(form)] = nullptr;
+            drop_all();  // all or nothing
             return finish(h, "hipGraphInstantiate", status);
         }
     }
@@ -1673,13 +1684,14 @@ int kudacuda_qwen2_model_replay(void* raw_model, int64_t steps, uint64_t stream)
     if (m == nullptr) {
         return 1;
     }
-    if (m->exec == nullptr) {
+    const size_t cap = static_cast<size_t>(kc::step_defer_cap(*m));
+    if (m->execs[cap] == nullptr) {
         m->handle->set_error("qwen2_model_replay called before qwen2_model_capture");
         return 1;
     }
     for (int64_t i = 0; i < steps; ++i) {
-        const bool long_ctx = m->exec_long != nullptr && kc::long_step(*m, m->host_step);
-        const hipError_t status = hipGraphLaunch(long_ctx ? m->exec_long : m->exec, as_stream(stream));
+        hipGraphExec_t e = m->execs[static_cast<size_t>(kc::step_form(*m, m->host_step))];
+        const hipError_t status = hipGraphLaunch(e != nullptr ? e : m->execs[cap], as_stream(stream));
         if (status != hipSuccess) {
             return finish(m->handle, "hipGraphLaunch", status);
         }

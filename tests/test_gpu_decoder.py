@@ -154,17 +154,24 @@ def test_long_context_decode_matches_oracle(torch_gpu, native, prompt_len, new, 
 @pytest.mark.parametrize("start,capacity,mode", [
     (2100, 4096, "eager"), (4200, 8192, "eager"),
     (700, 1024, "graph"), (700, 1024, "graph, position unknown"), (189, 1024, "graph"),
+    (61, 1024, "graph"), (100, 1024, "graph, position stale low"), (100, 1024, "graph, position stale high"),
+    (700, 1024, "graph, position stale low"),
 ])
 def test_decode_from_a_seeded_long_cache_matches_oracle(torch_gpu, native, start, capacity, mode):
     # Longer splits inside the decode step: both models get the same random
     # cache rows 0..start-1 and decode from position start.  At 2100+ tokens
     # the step's plan makes 22 splits of three 32-token rounds, at 4200 of an
     # 8192-row cache 27 splits of five rounds, at 700 22 one-round splits.
-    # Past 6 splits (192 cached tokens) the step runs in its long-cache form
-    # (gqa_merge_kernel merges the splits, o_proj is a plain GEMV) when the
-    # library knows the position, in the short form (the attention kernel's
-    # ticket merges them) when it does not; from 189 the steps cross that
-    # boundary (kv_len 190 .. 195).  Every form must equal the oracle.
+    # The step runs in the form for the split count at the position the
+    # library believes is next: up to 6 splits a form whose o_proj merges
+    # exactly that many (from 61 the steps cross 2 -> 3 splits), past 6
+    # splits (192 cached tokens) the long-cache form (gqa_merge_kernel merges
+    # the splits, o_proj is a plain GEMV; from 189 the steps cross into it),
+    # and the 6-split form when the position is unknown (past 6 splits the
+    # attention kernel's ticket merges).  A stale position picks a form made
+    # for another length: too few o_proj slots (the attention kernel then
+    # merges by its ticket) or the long form at a short cache.  Every case
+    # must equal the oracle.
     torch = torch_gpu
     new = 6
     kw = dict(num_layers=2, vocab=4096, kv_capacity=capacity, token_capacity=capacity)
@@ -189,6 +196,10 @@ def test_decode_from_a_seeded_long_cache_matches_oracle(torch_gpu, native, start
             gpu.capture()
         if mode == "graph, position unknown":
             gpu._set_position(-1)
+        elif mode == "graph, position stale low":
+            gpu._set_position(0)  # the one-split form
+        elif mode == "graph, position stale high":
+            gpu._set_position(capacity - 8)  # the long-cache form
         print(f"seeded cache: start {start}, capacity {capacity}, {mode}", flush=True)
         for step in range(new):
             if mode == "eager":

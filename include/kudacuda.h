@@ -363,7 +363,7 @@ KUDACUDA_API void* kudacuda_qwen2_model_create(void* handle, int64_t num_layers,
 KUDACUDA_API int kudacuda_qwen2_model_step(void* model, uint64_t stream);
 /* Capture one decode step into the model's own hipGraphs (replaces any
  * previous ones) and instantiate them; the step is not executed.  The step
- * is captured in one form per attention split count o_proj can merge (1..6
+ * is captured in one form per attention split count o_proj can merge (1..16
  * splits of 32 cached tokens per KV head, o_proj requesting exactly that
  * many) and, when the cache can hold more, in a form for long caches
  * (attention merged by its own kernel, o_proj as a plain GEMV). */

@@ -27,12 +27,14 @@ enum class RowMode { kGemv = 0, kQkv = 1, kQkvRope = 2, kSwiGlu = 3 };
 constexpr int kGqaPartialStride = 130;
 constexpr int kGqaRoundTokens = 32;      // tokens of one round (one per 16-lane group of a block)
 constexpr int64_t kGqaSplitCap = 256;    // most splits per KV head of an uncapped plan
-// Most splits a consumer merges.  Each slot costs o_proj ~0.1 us per layer
-// at every length (its requests re-read split 0 when fewer are live); 6
-// covers one-round splits up to 192 tokens, after which the attention
-// kernel's ticket merge takes over.
-constexpr int kGqaMaxDefer = 6;
+// Most splits a consumer merges.  Each slot costs o_proj ~0.1 us per layer,
+// so the decode step is captured once per slot count and a step pays only
+// for the splits at its length; 16 covers one-round splits up to 512 cached
+// tokens (a consumer's plain split-order sum equals the grouped one only up
+// to kGqaMergeGroup splits), past which the merge kernel takes over.
+constexpr int kGqaMaxDefer = 16;
 constexpr int kGqaMergeGroup = 16;       // merges sum splits in groups of this many, then the groups
+static_assert(kGqaMaxDefer <= kGqaMergeGroup, "a deferred merge is one group: its sum is the grouped sum");
 // Split cap of the decode step's plan: every split count it can reach is
 // merged by o_proj (deferred) or by the in-kernel ticket, so the step's graph
 // holds no merge-kernel node.

@@ -739,6 +739,23 @@ __global__ __launch_bounds__(256) void nf4_dequantize_kernel(const uint8_t* pack
     }
 }
 
+// The o_proj GEMV with the attention merge prologue for k deferral slots:
+// instantiations K = 1 .. kGqaMaxDefer, tried in turn.
+template <typename T, RowMode MODE, int TPW, int K>
+hipError_t launch_attn_rows(int k, dim3 grid, const void* const* h, const Nf4RowsArgs& a, int64_t ntasks,
+                            hipStream_t stream) {
+    if constexpr (K > kGqaMaxDefer) {
+        return hipErrorInvalidValue;
+    } else {
+        if (k != K) {
+            return launch_attn_rows<T, MODE, TPW, K + 1>(k, grid, h, a, ntasks, stream);
+        }
+        hipLaunchKernelGGL((nf4_rows2048_kernel<T, MODE, TPW, K>), grid, dim3(kRowsThreads), 0, stream, h[0], h[1],
+                           h[2], h[3], h[4], h[5], a, ntasks);
+        return hipGetLastError();
+    }
+}
+
 template <typename T, RowMode MODE, int TPW>
 hipError_t launch_rows_tpw(const Nf4RowsArgs& a, int64_t ntasks, int64_t blocks, hipStream_t stream) {
     const void* h[6];
@@ -747,23 +764,7 @@ hipError_t launch_rows_tpw(const Nf4RowsArgs& a, int64_t ntasks, int64_t blocks,
     if constexpr (MODE == RowMode::kGemv && TPW == 1) {
         if (a.attn.partials != nullptr) {
             // one instantiation per deferral slot count (1..kGqaMaxDefer, checked by the caller)
-            static_assert(kGqaMaxDefer == 6, "one case per slot count");
-            switch (a.attn.defer_max) {
-#define KC_ATTN_CASE(K)                                                                                      \
-    case K:                                                                                                  \
-        hipLaunchKernelGGL((nf4_rows2048_kernel<T, MODE, TPW, K>), grid, dim3(kRowsThreads), 0, stream, h[0], \
-                           h[1], h[2], h[3], h[4], h[5], a, ntasks);                                         \
-        return hipGetLastError();
-                KC_ATTN_CASE(1)
-                KC_ATTN_CASE(2)
-                KC_ATTN_CASE(3)
-                KC_ATTN_CASE(4)
-                KC_ATTN_CASE(5)
-                KC_ATTN_CASE(6)
-#undef KC_ATTN_CASE
-                default:
-                    return hipErrorInvalidValue;
-            }
+            return launch_attn_rows<T, MODE, TPW, 1>(static_cast<int>(a.attn.defer_max), grid, h, a, ntasks, stream);
         }
     }
     if constexpr (MODE == RowMode::kSwiGlu) {

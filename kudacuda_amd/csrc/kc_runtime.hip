@@ -789,13 +789,18 @@ hipError_t model_prefill(const Model& m, uint8_t* ws, int64_t start, int64_t cou
     return launch_lm_head_argmax(a, stream);
 }
 
+// The form of a step whose position the host does not know: six deferral
+// slots (one-round splits up to 192 cached tokens), the plan callers had
+// before positions were tracked.
+constexpr int64_t kUnknownStepForm = 6;
+
 // The fastest form for the step at `step` (kv_len step + 1): the split
-// count itself while o_proj merges it, form 0 past the cap, the cap when the
-// step is unknown.
+// count itself while o_proj merges it, form 0 past the cap, kUnknownStepForm
+// (or the cap, if smaller) when the step is unknown.
 int step_form(const Model& m, int64_t step) {
     const int64_t cap = step_defer_cap(m);
     if (step < 0) {
-        return static_cast<int>(cap);
+        return static_cast<int>(cap < kUnknownStepForm ? cap : kUnknownStepForm);
     }
     GqaArgs plan;
     set_gqa_plan(plan, m.capacity, kGqaStepSplits);
@@ -1684,14 +1689,14 @@ int kudacuda_qwen2_model_replay(void* raw_model, int64_t steps, uint64_t stream)
     if (m == nullptr) {
         return 1;
     }
-    const size_t cap = static_cast<size_t>(kc::step_defer_cap(*m));
-    if (m->execs[cap] == nullptr) {
+    const size_t fallback = static_cast<size_t>(kc::step_form(*m, -1));
+    if (m->execs[fallback] == nullptr) {
         m->handle->set_error("qwen2_model_replay called before qwen2_model_capture");
         return 1;
     }
     for (int64_t i = 0; i < steps; ++i) {
         hipGraphExec_t e = m->execs[static_cast<size_t>(kc::step_form(*m, m->host_step))];
-        const hipError_t status = hipGraphLaunch(e != nullptr ? e : m->execs[cap], as_stream(stream));
+        const hipError_t status = hipGraphLaunch(e != nullptr ? e : m->execs[fallback], as_stream(stream));
         if (status != hipSuccess) {
             return finish(m->handle, "hipGraphLaunch", status);
         }
@@ -1732,7 +1737,7 @@ int kudacuda_qwen2_model_time_op(void* raw_model, int64_t op, int64_t iters, uin
     hipError_t status = hipStreamBeginCapture(s, hipStreamCaptureModeGlobal);
     hipError_t launch = hipSuccess;
     for (int64_t i = 0; i < iters && status == hipSuccess && launch == hipSuccess; ++i) {
-        launch = kc::model_op(*m, static_cast<int>(op), i % m->num_layers, false, s);
+        launch = kc::model_op(*m, static_cast<int>(op), i % m->num_layers, false, s, kc::step_form(*m, m->host_step));
     }
     if (status == hipSuccess) {
         status = hipStreamEndCapture(s, &graph);

@@ -153,9 +153,9 @@ def test_long_context_decode_matches_oracle(torch_gpu, native, prompt_len, new, 
 
 @pytest.mark.parametrize("start,capacity,mode", [
     (2100, 4096, "eager"), (4200, 8192, "eager"),
-    (700, 1024, "graph"), (700, 1024, "graph, position unknown"), (189, 1024, "graph"),
+    (700, 1024, "graph"), (700, 1024, "graph, position unknown"), (189, 1024, "graph"), (509, 1024, "graph"),
     (61, 1024, "graph"), (100, 1024, "graph, position stale low"), (100, 1024, "graph, position stale high"),
-    (700, 1024, "graph, position stale low"),
+    (700, 1024, "graph, position stale low"), (300, 1024, "graph, position unknown"),
 ])
 def test_decode_from_a_seeded_long_cache_matches_oracle(torch_gpu, native, start, capacity, mode):
     # Longer splits inside the decode step: both models get the same random
@@ -163,15 +163,15 @@ def test_decode_from_a_seeded_long_cache_matches_oracle(torch_gpu, native, start
     # the step's plan makes 22 splits of three 32-token rounds, at 4200 of an
     # 8192-row cache 27 splits of five rounds, at 700 22 one-round splits.
     # The step runs in the form for the split count at the position the
-    # library believes is next: up to 6 splits a form whose o_proj merges
-    # exactly that many (from 61 the steps cross 2 -> 3 splits), past 6
-    # splits (192 cached tokens) the long-cache form (gqa_merge_kernel merges
-    # the splits, o_proj is a plain GEMV; from 189 the steps cross into it),
-    # and the 6-split form when the position is unknown (past 6 splits the
-    # attention kernel's ticket merges).  A stale position picks a form made
-    # for another length: too few o_proj slots (the attention kernel then
-    # merges by its ticket) or the long form at a short cache.  Every case
-    # must equal the oracle.
+    # library believes is next: up to 16 splits a form whose o_proj merges
+    # exactly that many (from 61 the steps cross 2 -> 3 splits, from 189
+    # 6 -> 7), past 16 splits (512 cached tokens) the long-cache form
+    # (gqa_merge_kernel merges the splits, o_proj is a plain GEMV; from 509
+    # the steps cross into it), and the 6-split form when the position is
+    # unknown (past 6 splits the attention kernel's ticket merges: 300 and
+    # 700 tokens).  A stale position picks a form made for another length:
+    # too few o_proj slots (the attention kernel then merges by its ticket)
+    # or the long form at a short cache.  Every case must equal the oracle.
     torch = torch_gpu
     new = 6
     kw = dict(num_layers=2, vocab=4096, kv_capacity=capacity, token_capacity=capacity)

@@ -479,10 +479,16 @@ int64_t step_defer_cap(const Model& m) {
     return model_defer(plan.max_splits);
 }
 
+// The form of a step whose position the host does not know: six deferral
+// slots (one-round splits up to 192 cached tokens), the plan callers had
+// before positions were tracked.
+constexpr int64_t kUnknownStepForm = 6;
+
 // form (ops 1 and 2 only): k = 1 .. step_defer_cap -- attention leaves up to
 // k splits to o_proj, whose merge prologue requests exactly k split slots,
-// and merges more by its own ticket (no merge launch in the graph); -1: k =
-// the cap; 0 -- the form for caches whose split count exceeds the cap:
+// and merges more by its own ticket (no merge launch in the graph); -1: the
+// unknown-position form, kUnknownStepForm (or the cap, if smaller); 0 -- the
+// form for caches whose split count exceeds the cap:
 // attention's partials all go to gqa_merge_kernel (one more launch, parallel
 // over heads and dims) and o_proj reads the merged vector as a plain GEMV.
 // Every form merges by the same rule in the same order: identical results at
@@ -490,7 +496,9 @@ int64_t step_defer_cap(const Model& m) {
 hipError_t model_op(const Model& m, int op, int64_t layer, bool bookkeeping, hipStream_t stream,
                     int form = -1) {
     const bool long_ctx = form == 0;
-    const int64_t defer = form < 0 || form > step_defer_cap(m) ? step_defer_cap(m) : form;
+    const int64_t cap = step_defer_cap(m);
+    const int64_t want = form < 0 ? kUnknownStepForm : form;
+    const int64_t defer = want < cap ? want : cap;
     const auto& L = m.layers[static_cast<size_t>(layer)];
     const auto& G = m.g;
     switch (op) {
@@ -788,11 +796,6 @@ hipError_t model_prefill(const Model& m, uint8_t* ws, int64_t start, int64_t cou
     a.tokens = ptr<int32_t>(G[KUDACUDA_QWEN2_TOKENS]);
     return launch_lm_head_argmax(a, stream);
 }
-
-// The form of a step whose position the host does not know: six deferral
-// slots (one-round splits up to 192 cached tokens), the plan callers had
-// before positions were tracked.
-constexpr int64_t kUnknownStepForm = 6;
 
 // The fastest form for the step at `step` (kv_len step + 1): the split
 // count itself while o_proj merges it, form 0 past the cap, kUnknownStepForm

@@ -39,7 +39,7 @@
 // splits at this L:
 //   * up to defer_max (the decode step sets it): left for the consumer, the
 //     o_proj row kernel, which merges them while its weight rows stream in;
-//   * one split: finished in place, out = acc*1 / (sum*1), the general merge
+//   * one split: finished in place, out = acc*1 * (1 / (sum*1)), the general merge
 //     with weight exp2(0) = 1;
 //   * up to ticket_max (<= kInKernelSplits): merged by the last block of the
 //     KV head to finish (an agent-scope acquire-release ticket, reset by that block,
@@ -49,7 +49,10 @@
 //     ticket_max splits; it returns at once when L needs fewer.
 // Every merge computes M = max over splits and w_s = exp2(m_s - M), sums
 // fma(l_s, w_s, .) and fma(acc_s, w_s, .) over groups of kGqaMergeGroup
-// consecutive splits in order, then adds the group sums in order, and divides.
+// consecutive splits in order, then adds the group sums in order, and scales
+// the sums by one correctly rounded reciprocal of l (acc * (1 / l): one
+// division per output instead of one per element where a thread finishes
+// several, o_proj's merge prologue 3.79 -> 3.60 us).
 // The result depends only on (inputs, kv_len, split_cap).
 //
 // Math follows the reference's split-KV workspace kernels
@@ -198,7 +201,7 @@ __device__ __forceinline__ void ticket_merge(const GqaArgs& a, const float* part
                 o = o + og;
             }
         }
-        a.out[(g * kHeadsPerGroup + hl) * kDim + idx % kDim] = T::store(o / lt);
+        a.out[(g * kHeadsPerGroup + hl) * kDim + idx % kDim] = T::store(o * (1.0f / lt));
     }
 }
 
@@ -418,8 +421,9 @@ void gqa_partial_kernel(const uint16_t* k_rows, const uint16_t* v_rows, const ui
         // single split: the general merge with weight exp2(M - M) = 1
         const float w = exp2_fixed(s_M[ph] - s_M[ph]);
         const float lt = fmaf(s_L[ph], w, 0.0f);
-        const uint32_t lo = T::store(fmaf(acc0, w, 0.0f) / lt);
-        const uint32_t hi = T::store(fmaf(acc1, w, 0.0f) / lt);
+        const float rl = 1.0f / lt;
+        const uint32_t lo = T::store(fmaf(acc0, w, 0.0f) * rl);
+        const uint32_t hi = T::store(fmaf(acc1, w, 0.0f) * rl);
         *reinterpret_cast<uint32_t*>(a.out + (g * kHeadsPerGroup + ph) * kDim + da) = lo | (hi << 16);
         return;
     }
@@ -582,7 +586,7 @@ __global__ __launch_bounds__(256) void gqa_merge_kernel(GqaArgs a) {
             o = j < ngroups ? o + go[j] : o;
             lt = j < ngroups ? lt + gl[j] : lt;
         }
-        a.out[static_cast<int64_t>(h) * kDim + d0 + d] = T::store(o / lt);
+        a.out[static_cast<int64_t>(h) * kDim + d0 + d] = T::store(o * (1.0f / lt));
     }
 }
 

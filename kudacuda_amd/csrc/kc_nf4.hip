@@ -253,7 +253,7 @@ struct RowsHot {
 // ATTN > 0 (kGemv only): x is the output of split-KV attention.  When the
 // partials were left unmerged (split count <= attn.defer_max = ATTN), thread t
 // merges head t/16, dims 8(t%16)..+7: M = max of the split maxima, weights
-// exp2(m_s - M), sum and acc accumulated in split order, x = T(acc / sum) --
+// exp2(m_s - M), sum and acc accumulated in split order, x = T(acc * (1 / sum)) --
 // the attention kernel's own merge -- into LDS before the block barrier.
 // The kv_len word, the partials and x (used when the attention merged
 // itself) are requested before the weight rows.
@@ -419,10 +419,11 @@ __global__ __launch_bounds__(NTH) void nf4_rows2048_kernel(const void* h0, const
                 }
             }
             uint32_t packed[4];
+            const float rl = 1.0f / lt;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                packed[j] = static_cast<uint32_t>(T::store(o[2 * j] / lt)) |
-                            (static_cast<uint32_t>(T::store(o[2 * j + 1] / lt)) << 16);
+                packed[j] = static_cast<uint32_t>(T::store(o[2 * j] * rl)) |
+                            (static_cast<uint32_t>(T::store(o[2 * j + 1] * rl)) << 16);
             }
             const uint4 xm = make_uint4(packed[0], packed[1], packed[2], packed[3]);
             reinterpret_cast<uint4*>(s_xa)[threadIdx.x] = xm;

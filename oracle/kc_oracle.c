@@ -430,7 +430,8 @@ static void gqa_scores(int act, const float qf[8][128], const uint16_t* krow, fl
  * l = l*r then + w_t in token order, acc = acc*r then fma(w_t, v_t, acc) in
  * token order.  The split partials are merged with w_s = exp2(m_s - M) in
  * groups of GQA_MERGE_GROUP splits (fma in split order), the group sums added
- * in order. */
+ * in order, and the output is acc * (1 / l) (one correctly rounded reciprocal,
+ * then a product, as every merge site of the kernels computes it). */
 KCO_API void kco_gqa(int act, const uint16_t* q, const uint16_t* kc, const uint16_t* vc, int64_t capacity,
                      int64_t L, int64_t split_cap, float qk_scale_log2, uint16_t* out) {
     if (L > capacity) L = capacity;
@@ -515,7 +516,7 @@ KCO_API void kco_gqa(int act, const uint16_t* q, const uint16_t* kc, const uint1
                     o = o + og;
                 }
             }
-            out[h * 128 + d] = act_store(act, o / lt);
+            out[h * 128 + d] = act_store(act, o * (1.0f / lt));
         }
     }
     free(part);

@@ -8,7 +8,7 @@ emits a token, the SHA-256 of the bf16 logits and of the final hidden state
 must equal the oracle's (tests/golden/decode_qwen25_3b_nf4.json, written by
 tests/golden/make_decode_golden.py from oracle/kc_oracle.c), and so must the
 128 token ids: the reference's headline parity claim, exact greedy tokens
-over a 128-token decode (README.md:36-39).  Six of the 128 steps have an exact
+over a 128-token decode (README.md:36-39).  Three of the 128 steps have an exact
 bf16 tie between the top two logits; there the token is fixed by the
 lowest-index rule and the bit-identical logits, which only a bit-exact
 oracle can pin.
@@ -162,7 +162,7 @@ def test_config5_prefill_matches_the_sequential_decode_cache(torch_gpu, native):
             layer["value_cache"].zero_()
         model.prefill(prompt)
         model.stream.synchronize()
-        assert int(host(model.tokens)[p]) == golden["tokens"][0]  # golden margin 0.078 at this token
+        assert int(host(model.tokens)[p]) == golden["tokens"][0]  # golden margin 0.109 at this token
         assert int(host(model.control)[0]) == p
         ratios = []
         for li, (layer, (k_seq, v_seq), (k_pt, v_pt)) in enumerate(zip(model.layers, seq, perturbed)):
